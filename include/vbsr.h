@@ -1,0 +1,167 @@
+/*
+ * vbsr.h -- C ABI of the MI355X VBSR SpMM library (libvarblockspmm_amd.so).
+ *
+ * Computes FP32 C = A * B for a packed variable-block sparse-row matrix A
+ * (block heights/widths in {8,16,...,64}, blocks column-major, packed without
+ * padding) and dense column-major panels B (K x rhs, ld = K) and
+ * C (M x rhs, ld = M), rhs in {8,16,32,64}.
+ *
+ * This is the drop-in boundary for the reference's C++ API
+ * (King-Clawthorne/VarBlockSpMM, include/varblockspmm/vbsr.hpp).  Each entry
+ * point names the reference declaration it replaces.  Plain pointers, sizes
+ * and status codes only; no C++ exception crosses it.  The C++ mirror of the
+ * reference API is include/varblockspmm/vbsr.hpp (header-only, over this ABI).
+ *
+ * Errors: every function returning int returns VBSR_OK (0),
+ * VBSR_INVALID_ARGUMENT (1) where the reference throws std::invalid_argument,
+ * or VBSR_RUNTIME_ERROR (2) where it throws std::runtime_error (HIP errors,
+ * launch errors, allocation failures).  vbsr_last_error() returns the message
+ * of the calling thread's last failure.
+ *
+ * Execution: vbsr_plan_execute and the launchers only enqueue kernels on the
+ * given stream; they never synchronise, never allocate and use no workspace.
+ * B and C must not alias.  C is fully overwritten.  Results are bit-identical
+ * from run to run (no atomics, fixed accumulation order).
+ */
+#ifndef VARBLOCKSPMM_AMD_VBSR_H
+#define VARBLOCKSPMM_AMD_VBSR_H
+
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum vbsr_status { VBSR_OK = 0, VBSR_INVALID_ARGUMENT = 1, VBSR_RUNTIME_ERROR = 2 };
+
+/* Host VBSR matrix, field for field the reference HostMatrix
+ * (vbsr.hpp:16-29), with each std::vector given as pointer + length. */
+typedef struct vbsr_host_view {
+  int32_t block_rows, block_cols;
+  const int32_t* row_ptr;        int64_t row_ptr_len;        /* block_rows + 1 */
+  const int32_t* block_col;      int64_t block_col_len;      /* nnzb */
+  const int32_t* row_size;       int64_t row_size_len;       /* block_rows */
+  const int32_t* col_size;       int64_t col_size_len;       /* block_cols */
+  const int64_t* row_scalar_off; int64_t row_scalar_off_len; /* block_rows + 1 */
+  const int64_t* col_scalar_off; int64_t col_scalar_off_len; /* block_cols + 1 */
+  const int64_t* value_off;      int64_t value_off_len;      /* nnzb + 1 */
+  const float* values;           int64_t values_len;         /* sum h*w */
+} vbsr_host_view;
+
+/* Non-owning device view; same fields and meaning as the reference
+ * DeviceMatrix (vbsr.hpp:32-38).  All pointers are device pointers. */
+typedef struct vbsr_device_view {
+  int32_t block_rows, block_cols, nnzb;
+  int64_t scalar_rows, scalar_cols;
+  const int32_t *row_ptr, *block_col, *row_size, *col_size;
+  const int64_t *row_scalar_off, *col_scalar_off, *value_off;
+  const float* values;
+} vbsr_device_view;
+
+/* Block-size distributions: 0..3 are the reference Distribution enumerators
+ * (vbsr.hpp:67; generator.cpp:14-30).  4 and 5 are extensions used by the
+ * benchmark configurations: sizes {8,64} with p = 1/2 each, and sizes
+ * {8,...,64} with the column partition equal to the row partition. */
+enum vbsr_distribution {
+  VBSR_DIST_UNIFORM = 0,
+  VBSR_DIST_LOW_VARIANCE = 1,
+  VBSR_DIST_HIGH_VARIANCE = 2,
+  VBSR_DIST_BIMODAL = 3,
+  VBSR_DIST_BIMODAL_8_OR_64 = 4,
+  VBSR_DIST_TIED_8_TO_64 = 5
+};
+
+/* Column patterns: the reference's random and cyclic-local patterns
+ * (generator.cpp:62-66; `local_columns`), plus a clamped local pattern:
+ * column = clamp(min(i, C-1) + e() % (2d+1) - d, 0, C-1). */
+enum vbsr_locality { VBSR_LOCALITY_RANDOM = 0, VBSR_LOCALITY_LOCAL = 1, VBSR_LOCALITY_LOCAL_CLAMPED = 2 };
+
+/* GeneratorOptions (vbsr.hpp:70-76); `locality` replaces the reference's
+ * `bool local_columns` (1 == true, 0 == false). */
+typedef struct vbsr_generator_options {
+  int32_t block_rows, block_cols, degree, rhs_width;
+  int32_t distribution; /* enum vbsr_distribution */
+  int32_t locality;     /* enum vbsr_locality */
+  uint64_t seed;
+} vbsr_generator_options;
+
+/* Kernel (vbsr.hpp:91) and PlanOptions (vbsr.hpp:94-97). */
+enum vbsr_kernel { VBSR_KERNEL_AUTO = 0, VBSR_KERNEL_ROW_OWNED = 1, VBSR_KERNEL_SPLIT_ROW = 2 };
+typedef struct vbsr_plan_options {
+  int32_t rhs_width;
+  int32_t kernel; /* enum vbsr_kernel */
+} vbsr_plan_options;
+
+typedef struct vbsr_host_matrix vbsr_host_matrix; /* owning host matrix (generator output) */
+typedef struct vbsr_matrix vbsr_matrix;           /* owning device matrix: reference Matrix */
+typedef struct vbsr_plan vbsr_plan;               /* execution plan: reference Plan */
+
+/* Message of the calling thread's most recent failure ("" if none). */
+const char* vbsr_last_error(void);
+
+/* HostMatrix::validate (vbsr.hpp:28; vbsr.cpp:29-82): same accept/reject set. */
+int vbsr_validate(const vbsr_host_view* host);
+
+/* generate (vbsr.hpp:80; generator.cpp:7-88): same engine, same draw order,
+ * same matrices for the reference's distributions and localities. */
+int vbsr_generate(const vbsr_generator_options* options, vbsr_host_matrix** out);
+/* Views the arrays of a generated matrix (valid until it is destroyed). */
+int vbsr_host_matrix_view(const vbsr_host_matrix* matrix, vbsr_host_view* out);
+void vbsr_host_matrix_destroy(vbsr_host_matrix* matrix);
+
+/* The reference test's B generator (tests/test_main.cpp:42-51):
+ * std::mt19937{unsigned(seed)} feeding uniform_real_distribution<float>(-1,1)
+ * into out[0..count). */
+int vbsr_make_random_input(int64_t count, uint64_t seed, float* out);
+
+/* Matrix(const HostMatrix&) (vbsr.hpp:44; vbsr.cpp:84-113): validates, then
+ * copies every array to the current HIP device and builds the row schedule.
+ * Additionally rejects (VBSR_INVALID_ARGUMENT) row/col scalar offsets that do
+ * not start at 0, which the reference accepts but which would leave C rows
+ * unwritten or index outside B and C. */
+int vbsr_matrix_create(const vbsr_host_view* host, vbsr_matrix** out);
+/* ~Matrix (vbsr.cpp:114-127).  Null is a no-op. */
+void vbsr_matrix_destroy(vbsr_matrix* matrix);
+/* Matrix::device_view (vbsr.hpp:51; vbsr.cpp:163-166). */
+int vbsr_matrix_device_view(const vbsr_matrix* matrix, vbsr_device_view* out);
+/* Matrix::scalar_rows / scalar_cols (vbsr.hpp:52-53). */
+int64_t vbsr_matrix_scalar_rows(const vbsr_matrix* matrix);
+int64_t vbsr_matrix_scalar_cols(const vbsr_matrix* matrix);
+/* The matrix's row schedule: a device permutation of [0, block_rows) that
+ * orders block rows by decreasing work (the counterpart of the reference's
+ * private row_shape_order, vbsr.cpp:96-102).  Pass it to
+ * vbsr_launch_row_owned. */
+int vbsr_matrix_row_schedule(const vbsr_matrix* matrix, const int32_t** row_order);
+
+/* Plan(const Matrix&, PlanOptions) (vbsr.hpp:106; plan.cpp:5-18): rejects
+ * rhs_width outside {8,16,32,64} and VBSR_KERNEL_SPLIT_ROW.  The plan views
+ * the matrix, which must outlive it. */
+int vbsr_plan_create(const vbsr_matrix* matrix, const vbsr_plan_options* options, vbsr_plan** out);
+void vbsr_plan_destroy(vbsr_plan* plan);
+/* Plan::execute (vbsr.hpp:110; plan.cpp:19-22): enqueues C = A * B on
+ * `stream` (0 = null stream). */
+int vbsr_plan_execute(const vbsr_plan* plan, const float* B, float* C, hipStream_t stream);
+/* Plan::launch_count (vbsr.hpp:112; plan.cpp:23-31): kernels enqueued by one
+ * vbsr_plan_execute. */
+int vbsr_plan_launch_count(const vbsr_plan* plan);
+
+/* launch_row_owned (vbsr.hpp:158-159; row_owned.cu:397-423): the tuned
+ * row-owned kernels for `rhs`.  `row_order` is a device permutation of the
+ * block rows (e.g. from vbsr_matrix_row_schedule) or NULL for natural order;
+ * it changes only the scheduling, never the result. */
+int vbsr_launch_row_owned(const vbsr_device_view* matrix, const int32_t* row_order, const float* B,
+                          float* C, int32_t rhs, hipStream_t stream);
+
+/* launch_row_owned_scalar (vbsr.hpp:161; row_owned.cu:376-395): one output
+ * per lane, accumulated with fmaf over blocks in row_ptr order and k
+ * ascending from 0 -- the reference kernels' exact order, so its results are
+ * bit-identical to theirs. */
+int vbsr_launch_row_owned_scalar(const vbsr_device_view* matrix, const float* B, float* C,
+                                 int32_t rhs, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

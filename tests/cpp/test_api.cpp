@@ -1,0 +1,196 @@
+// C++ API test: the reference's test program (tests/test_main.cpp) restated
+// against this library's C++ API (include/varblockspmm/vbsr.hpp), with the
+// gaps it leaves closed: outputs are poisoned with NaN before every run, the
+// order-preserving kernel is checked bit for bit against the oracle's fmaf
+// emulation, repeated runs must be bit-identical, and the stricter
+// normwise/elementwise bounds are checked too.  The reference values come
+// from the CPU oracle (oracle/vbsr_oracle.h).  Needs a GPU.
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstring>
+#include <functional>
+#include <iostream>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include <varblockspmm/vbsr.hpp>
+
+extern "C" {
+#include "vbsr_oracle.h"
+}
+
+namespace {
+
+void hip_ok(hipError_t status, const char* what) {
+  if (status != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(status));
+}
+
+orc_view oracle_view(const vbsr::HostMatrix& m) {
+  orc_view v{};
+  v.block_rows = m.block_rows;
+  v.block_cols = m.block_cols;
+  v.row_ptr = m.row_ptr.data(); v.row_ptr_len = int64_t(m.row_ptr.size());
+  v.block_col = m.block_col.data(); v.block_col_len = int64_t(m.block_col.size());
+  v.row_size = m.row_size.data(); v.row_size_len = int64_t(m.row_size.size());
+  v.col_size = m.col_size.data(); v.col_size_len = int64_t(m.col_size.size());
+  v.row_scalar_off = m.row_scalar_off.data(); v.row_scalar_off_len = int64_t(m.row_scalar_off.size());
+  v.col_scalar_off = m.col_scalar_off.data(); v.col_scalar_off_len = int64_t(m.col_scalar_off.size());
+  v.value_off = m.value_off.data(); v.value_off_len = int64_t(m.value_off.size());
+  v.values = m.values.data(); v.values_len = int64_t(m.values.size());
+  return v;
+}
+
+struct DeviceBuffer {
+  float* ptr{};
+  size_t count{};
+  explicit DeviceBuffer(size_t n) : count(n) { hip_ok(hipMalloc(&ptr, std::max<size_t>(n, 1) * sizeof(float)), "hipMalloc"); }
+  ~DeviceBuffer() { (void)hipFree(ptr); }
+  std::vector<float> read() const {
+    std::vector<float> out(count);
+    hip_ok(hipMemcpy(out.data(), ptr, count * sizeof(float), hipMemcpyDeviceToHost), "hipMemcpy D2H");
+    return out;
+  }
+  void poison() {
+    std::vector<float> nan(count, std::nanf(""));
+    hip_ok(hipMemcpy(ptr, nan.data(), count * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy H2D");
+  }
+};
+
+// Reference tolerance (tests/test_main.cpp:14-40) plus the library's bounds.
+void compare(const std::vector<float>& result, const std::vector<float>& reference,
+             const std::vector<double>& bound, const std::string& name) {
+  double max_err = 0, sq_err = 0, ref_norm = 0, ref_max = 0, bound_max = 0;
+  for (size_t i = 0; i < result.size(); ++i) {
+    if (!std::isfinite(result[i])) throw std::runtime_error(name + " produced NaN/Inf");
+    const double e = double(result[i]) - reference[i];
+    max_err = std::max(max_err, std::abs(e));
+    sq_err += e * e;
+    ref_norm += double(reference[i]) * reference[i];
+    ref_max = std::max(ref_max, std::abs(double(reference[i])));
+    bound_max = std::max(bound_max, bound[i]);
+  }
+  const double rel = std::sqrt(sq_err / (ref_norm + 1e-30));
+  const double normwise = max_err / (ref_max + 1e-30);
+  const double elementwise = max_err / (bound_max + 1e-30);
+  if (max_err > 5e-4 || rel > 5e-5 || normwise > 1e-5 || elementwise > 1e-6)
+    throw std::runtime_error(name + " mismatch: max=" + std::to_string(max_err) + " rel=" + std::to_string(rel) +
+                             " normwise=" + std::to_string(normwise) + " elementwise=" + std::to_string(elementwise));
+}
+
+void expect_invalid_argument(const std::function<void()>& op, const char* failure) {
+  try {
+    op();
+  } catch (const std::invalid_argument&) {
+    return;
+  }
+  throw std::runtime_error(failure);
+}
+
+// tests/test_main.cpp:116-143
+void run_negative_tests() {
+  vbsr::GeneratorOptions options;
+  options.block_rows = 4;
+  options.block_cols = 4;
+  options.degree = 2;
+  const vbsr::HostMatrix valid = vbsr::generate(options);
+  vbsr::HostMatrix bad = valid;
+  bad.row_ptr.back()++;
+  expect_invalid_argument([&] { bad.validate(); }, "malformed row_ptr accepted");
+  bad = valid;
+  bad.row_size[0] = 7;
+  expect_invalid_argument([&] { bad.validate(); }, "unsupported block size accepted");
+  expect_invalid_argument([&] { vbsr::Matrix m(bad); }, "Matrix accepted an invalid host matrix");
+  vbsr::Matrix device(valid);
+  expect_invalid_argument([&] { vbsr::Plan plan(device, {7, vbsr::Kernel::RowOwned}); }, "invalid RHS accepted");
+  expect_invalid_argument([&] { vbsr::Plan plan(device, {8, vbsr::Kernel::SplitRow}); }, "split-row accepted");
+  options.degree = 5;
+  expect_invalid_argument([&] { vbsr::generate(options); }, "degree > block_cols accepted");
+}
+
+// tests/test_main.cpp:61-105 for one case.
+void run_case(vbsr::Distribution distribution, int degree, int rhs, bool local, uint64_t seed) {
+  vbsr::GeneratorOptions options;
+  options.block_rows = 9;
+  options.block_cols = 17;
+  options.degree = degree;
+  options.distribution = distribution;
+  options.local_columns = local;
+  options.seed = seed;
+  const vbsr::HostMatrix host = vbsr::generate(options);
+  const orc_view ov = oracle_view(host);
+
+  std::vector<float> input(size_t(host.scalar_cols() * rhs));
+  orc_make_random_input(int64_t(input.size()), seed, input.data());
+  std::vector<float> reference(size_t(host.scalar_rows() * rhs)), emulated(reference.size());
+  std::vector<double> bound(reference.size());
+  orc_cpu_reference(&ov, input.data(), int64_t(input.size()), rhs, reference.data());
+  orc_fmaf_order(&ov, input.data(), int64_t(input.size()), rhs, emulated.data());
+  orc_abs_product_sum(&ov, input.data(), int64_t(input.size()), rhs, bound.data());
+
+  vbsr::Matrix device(host);
+  DeviceBuffer b(input.size()), c(reference.size());
+  hip_ok(hipMemcpy(b.ptr, input.data(), input.size() * sizeof(float), hipMemcpyHostToDevice), "upload B");
+  hipStream_t stream;
+  hip_ok(hipStreamCreate(&stream), "hipStreamCreate");
+
+  const std::string tag = " (degree " + std::to_string(degree) + ", rhs " + std::to_string(rhs) + ", seed " +
+                          std::to_string(seed) + ")";
+  vbsr::Plan plan(device, {rhs, vbsr::Kernel::RowOwned});
+  if (plan.launch_count() != 1) throw std::runtime_error("launch_count != 1" + tag);
+  c.poison();
+  plan.execute(b.ptr, c.ptr, stream);
+  hip_ok(hipStreamSynchronize(stream), "sync");
+  const std::vector<float> first = c.read();
+  compare(first, reference, bound, "row-owned MFMA" + tag);
+  c.poison();
+  plan.execute(b.ptr, c.ptr, stream);
+  hip_ok(hipStreamSynchronize(stream), "sync");
+  if (std::memcmp(first.data(), c.read().data(), first.size() * sizeof(float)) != 0)
+    throw std::runtime_error("row-owned MFMA not bit-identical across runs" + tag);
+
+  c.poison();
+  vbsr::launch_row_owned_scalar(device.device_view(), b.ptr, c.ptr, rhs, stream);
+  hip_ok(hipStreamSynchronize(stream), "sync");
+  const std::vector<float> scalar = c.read();
+  compare(scalar, reference, bound, "row-owned scalar" + tag);
+  if (std::memcmp(scalar.data(), emulated.data(), scalar.size() * sizeof(float)) != 0)
+    throw std::runtime_error("row-owned scalar differs from the fmaf-order emulation" + tag);
+
+  hip_ok(hipStreamDestroy(stream), "hipStreamDestroy");
+}
+
+// tests/test_main.cpp:145-161
+int run_parameter_matrix() {
+  const vbsr::Distribution distributions[] = {vbsr::Distribution::Uniform, vbsr::Distribution::LowVariance,
+                                              vbsr::Distribution::HighVariance, vbsr::Distribution::Bimodal};
+  const int degrees[] = {1, 4, 8, 16};
+  const int widths[] = {8, 16, 32, 64};
+  uint64_t seed = 11;
+  int cases = 0;
+  for (const auto distribution : distributions)
+    for (const int degree : degrees)
+      for (const int rhs : widths) {
+        run_case(distribution, degree, rhs, (seed & 1) != 0, seed);
+        ++seed;
+        ++cases;
+      }
+  return cases;
+}
+
+}  // namespace
+
+int main() {
+  try {
+    run_negative_tests();
+    const int cases = run_parameter_matrix();
+    std::cout << "PASS: negative tests + " << cases
+              << " parameter cases (MFMA plan + order-preserving kernel, non-default stream, NaN-poisoned C, "
+                 "bit-identical repeats)\n";
+    return 0;
+  } catch (const std::exception& error) {
+    std::cerr << "FAIL: " << error.what() << '\n';
+    return 1;
+  }
+}

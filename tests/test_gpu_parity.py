@@ -1,0 +1,286 @@
+"""GPU parity: the HIP kernels, called through the C ABI, against the CPU oracle.
+
+Bars (written per check below):
+  - MFMA row-owned path: within the reference test's tolerance
+    (max|err| <= 5e-4, rel-L2 <= 5e-5, tests/test_main.cpp:35) and the
+    library's bounds: normwise max|C - Cref| / max|Cref| <= 1e-5,
+    rel-L2 <= 1e-5, max|C - Cref| / max(sum |a||b|) <= 1e-6; bit-identical
+    across runs.
+  - Order-preserving kernel: bit-identical to the oracle's fmaf emulation of
+    the reference kernels' order.
+Every output buffer is poisoned with NaN before a run, so unwritten elements
+fail the check.
+"""
+
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+import oracle_ffi as o
+import varblockspmm_amd as vb
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+DEVICE = "cuda:0"
+
+NORMWISE_TOL = 1e-5
+REL_L2_TOL = 1e-5
+ELEMENTWISE_TOL = 1e-6
+
+
+def note(message):
+    print(message, flush=True)
+    sys.stdout.flush()
+
+
+def as_oracle(host):
+    return o.HostMatrix(host.block_rows, host.block_cols, **host.arrays())
+
+
+class Case:
+    """A host matrix with its device copy, B, and oracle results for one RHS width."""
+
+    def __init__(self, host, rhs, seed, stream=None):
+        self.host = host
+        self.rhs = rhs
+        self.oracle = as_oracle(host)
+        self.b = o.make_random_input(host.scalar_cols * rhs, seed)
+        self.matrix = vb.Matrix(host)
+        self.stream = stream if stream is not None else torch.cuda.Stream(device=DEVICE)
+        self.b_dev = torch.from_numpy(self.b).to(DEVICE)
+        self.c_dev = torch.empty(host.scalar_rows * rhs, dtype=torch.float32, device=DEVICE)
+        self._reference = None
+        self._bound = None
+
+    @property
+    def reference(self):
+        if self._reference is None:
+            self._reference = o.cpu_reference(self.oracle, self.b, self.rhs)
+        return self._reference
+
+    @property
+    def bound(self):
+        if self._bound is None:
+            self._bound = o.abs_product_sum(self.oracle, self.b, self.rhs)
+        return self._bound
+
+    def run(self, launch):
+        self.c_dev.fill_(float("nan"))
+        torch.cuda.current_stream(DEVICE).synchronize()
+        with torch.cuda.stream(self.stream):
+            launch()
+        self.stream.synchronize()
+        return self.c_dev.cpu().numpy().copy()
+
+    def run_plan(self, plan):
+        return self.run(lambda: plan.execute(self.b_dev, self.c_dev, self.stream))
+
+    def run_scalar(self):
+        view = self.matrix.device_view()
+        return self.run(lambda: vb.launch_row_owned_scalar(view, self.b_dev, self.c_dev, self.rhs, self.stream))
+
+    def check_tolerance(self, result, name):
+        assert np.all(np.isfinite(result)), f"{name}: NaN/Inf (unwritten or polluted outputs)"
+        max_abs, rel_l2, normwise, elementwise = o.parity_errors(result, self.reference, self.bound)
+        note(f"  {name}: max_abs={max_abs:.3g} rel_l2={rel_l2:.3g} normwise={normwise:.3g} "
+             f"elementwise={elementwise:.3g}")
+        assert max_abs <= 5e-4 and rel_l2 <= 5e-5, name  # tests/test_main.cpp:35
+        assert normwise <= NORMWISE_TOL and rel_l2 <= REL_L2_TOL and elementwise <= ELEMENTWISE_TOL, name
+
+    def close(self):
+        self.matrix.close()
+
+
+def reference_cases():
+    """tests/test_main.cpp:145-161: 4 distributions x degree {1,4,8,16} x RHS {8,16,32,64};
+    9 x 17 block grid; seed 11.. in order; local columns iff the seed is odd."""
+    cases = []
+    seed = 11
+    for distribution in ("uniform", "low", "high", "bimodal"):
+        for degree in (1, 4, 8, 16):
+            for rhs in (8, 16, 32, 64):
+                cases.append((distribution, degree, rhs, "local" if seed & 1 else "random", seed))
+                seed += 1
+    return cases
+
+
+@pytest.mark.parametrize("case", reference_cases(), ids=lambda c: "{}-d{}-n{}-{}-s{}".format(*c))
+def test_reference_parameter_matrix(case):
+    distribution, degree, rhs, locality, seed = case
+    note(f"case {case}")
+    c = Case(vb.generate(9, 17, degree, distribution, locality, seed), rhs, seed)
+    plan = vb.Plan(c.matrix, rhs, "row_owned")
+    assert plan.launch_count() == 1
+    first = c.run_plan(plan)
+    c.check_tolerance(first, "mfma")
+    np.testing.assert_array_equal(c.run_plan(plan), first, err_msg="mfma not bit-identical across runs")
+    scalar = c.run_scalar()
+    np.testing.assert_array_equal(scalar, o.fmaf_order(c.oracle, c.b, rhs), err_msg="scalar != fmaf emulation")
+    c.check_tolerance(scalar, "scalar")
+    c.close()
+
+
+BASELINE_CONFIGS = [
+    # (name, rows, degree, distribution, locality, rhs, seed)
+    ("config1-cpu-shape", 1024, 4, "high", "clamped", 8, 1),
+    ("config1-cyclic", 1024, 4, "high", "local", 8, 1),
+    ("config2", 1024, 8, "low", "random", 16, 2),
+    ("config3-metric", 4096, 8, "high", "random", 32, 1),
+    ("config3-n8", 4096, 8, "high", "random", 8, 1),
+    ("config3-n16", 4096, 8, "high", "random", 16, 1),
+    ("config3-n64", 4096, 8, "high", "random", 64, 1),
+    ("config4-literal-bimodal", 4096, 16, "bimodal8or64", "random", 64, 3),
+    ("config4-reference-bimodal", 4096, 16, "bimodal", "random", 64, 3),
+]
+
+
+@pytest.mark.parametrize("config", BASELINE_CONFIGS, ids=lambda c: c[0])
+def test_baseline_configs(config):
+    name, rows, degree, distribution, locality, rhs, seed = config
+    note(f"config {config}")
+    c = Case(vb.generate(rows, rows, degree, distribution, locality, seed), rhs, seed)
+    plan = vb.Plan(c.matrix, rhs)
+    first = c.run_plan(plan)
+    c.check_tolerance(first, name)
+    np.testing.assert_array_equal(c.run_plan(plan), first, err_msg="not bit-identical across runs")
+    c.close()
+
+
+@pytest.mark.parametrize("config", [("config2", 1024, 8, "low", "random", 16, 2),
+                                    ("config3-n8", 4096, 8, "high", "random", 8, 1)], ids=lambda c: c[0])
+def test_order_preserving_kernel_full_size(config):
+    name, rows, degree, distribution, locality, rhs, seed = config
+    note(f"scalar kernel {config}")
+    c = Case(vb.generate(rows, rows, degree, distribution, locality, seed), rhs, seed)
+    np.testing.assert_array_equal(c.run_scalar(), o.fmaf_order(c.oracle, c.b, rhs))
+    c.close()
+
+
+@pytest.mark.parametrize("rhs", [8, 16, 32, 64])
+def test_row_order_changes_no_bits(rhs):
+    note(f"row order rhs={rhs}")
+    c = Case(vb.generate(300, 280, 6, "high", "random", 5), rhs, 5)
+    view = c.matrix.device_view()
+    scheduled = c.run(lambda: vb.launch_row_owned(view, c.b_dev, c.c_dev, rhs, c.stream, c.matrix.row_schedule()))
+    natural = c.run(lambda: vb.launch_row_owned(view, c.b_dev, c.c_dev, rhs, c.stream, None))
+    np.testing.assert_array_equal(scheduled, natural)
+    plan = vb.Plan(c.matrix, rhs)
+    np.testing.assert_array_equal(c.run_plan(plan), scheduled)
+    c.check_tolerance(natural, "natural order")
+    c.close()
+
+
+def hand_made(row_size, col_size, rows_blocks, seed=0):
+    """A host matrix from per-row block-column lists (empty rows and repeats allowed)."""
+    rng = np.random.default_rng(seed)
+    row_ptr = np.concatenate([[0], np.cumsum([len(b) for b in rows_blocks])])
+    block_col = np.array([c for b in rows_blocks for c in b], dtype=np.int32)
+    owners = np.repeat(np.arange(len(row_size)), [len(b) for b in rows_blocks])
+    counts = np.array(row_size)[owners] * np.array(col_size)[block_col] if len(block_col) else np.zeros(0)
+    value_off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    return vb.HostMatrix(len(row_size), len(col_size), row_ptr=row_ptr, block_col=block_col, row_size=row_size,
+                         col_size=col_size, row_scalar_off=np.concatenate([[0], np.cumsum(row_size)]),
+                         col_scalar_off=np.concatenate([[0], np.cumsum(col_size)]), value_off=value_off,
+                         values=rng.uniform(-1, 1, int(value_off[-1])).astype(np.float32))
+
+
+EDGE_MATRICES = {
+    # empty rows, a repeated block column, unsorted columns, every height
+    "empty-repeat-unsorted": lambda: hand_made([8, 16, 24, 32, 40, 48, 56, 64], [8, 24, 64, 40, 16],
+                                                [[1, 1, 0], [], [4, 2], [0], [], [3, 2, 1, 0, 4], [2], [4, 4]]),
+    "all-empty": lambda: hand_made([8, 64, 24], [8, 8], [[], [], []]),
+    "single-row": lambda: hand_made([40], [56, 8, 64], [[0, 1, 2]]),
+    "all-8": lambda: hand_made([8] * 20, [8] * 20, [[(i + j) % 20 for j in range(5)] for i in range(20)]),
+    "all-64": lambda: hand_made([64] * 12, [64] * 12, [[(i * 5 + j) % 12 for j in range(4)] for i in range(12)]),
+    "narrow-wide": lambda: hand_made([8, 64] * 8, [64, 8] * 8, [[j for j in range(16) if (i + j) % 3 == 0]
+                                                                 for i in range(16)]),
+}
+
+
+@pytest.mark.parametrize("rhs", [8, 16, 32, 64])
+@pytest.mark.parametrize("name", list(EDGE_MATRICES))
+def test_edge_matrices(name, rhs):
+    note(f"edge {name} rhs={rhs}")
+    host = EDGE_MATRICES[name]()
+    host.validate()
+    c = Case(host, rhs, 17)
+    result = c.run_plan(vb.Plan(c.matrix, rhs))
+    c.check_tolerance(result, name)
+    empty = np.diff(host.row_ptr) == 0
+    out = result.reshape(rhs, host.scalar_rows)
+    for i in np.nonzero(empty)[0]:
+        assert np.all(out[:, host.row_scalar_off[i]:host.row_scalar_off[i + 1]] == 0.0)
+    np.testing.assert_array_equal(c.run_scalar(), o.fmaf_order(c.oracle, c.b, rhs))
+    c.close()
+
+
+@pytest.mark.parametrize("rhs", [8, 16, 32, 64])
+def test_unused_b_entries_never_reach_c(rhs):
+    """NaN in every B row that no block references (including the rows right
+    after each used 8-wide column and the panel's end) must not leak into C."""
+    note(f"unused-B NaN rhs={rhs}")
+    col_size = [8, 16, 8, 24, 8, 64, 8, 40, 8]
+    used = [0, 2, 4, 6, 8]  # 8-wide columns, each followed by an unused one
+    host = hand_made([16, 8, 48, 64, 24], col_size, [[0, 2], [4, 6, 8], [8], [0, 4, 6], [2, 8]], seed=3)
+    c = Case(host, rhs, 23)
+    offs = host.col_scalar_off
+    b = c.b.reshape(rhs, host.scalar_cols).copy()
+    clean = b.copy()
+    for j in range(len(col_size)):
+        if j not in used:
+            b[:, offs[j]:offs[j + 1]] = np.nan
+            clean[:, offs[j]:offs[j + 1]] = 0.0
+    c.b = clean.reshape(-1)
+    c.b_dev = torch.from_numpy(b.reshape(-1).copy()).to(DEVICE)
+    c.check_tolerance(c.run_plan(vb.Plan(c.matrix, rhs)), "nan-guarded")
+    np.testing.assert_array_equal(c.run_scalar(), o.fmaf_order(c.oracle, c.b, rhs))
+    c.close()
+
+
+def test_device_matrix_errors():
+    note("device errors")
+    host = vb.generate(6, 6, 2, "high", "random", 1)
+    bad = host.copy()
+    bad.row_size[0] = 7
+    with pytest.raises(ValueError):
+        vb.Matrix(bad)
+    shifted = host.copy()
+    shifted.row_scalar_off = shifted.row_scalar_off + 8
+    shifted.validate()  # accepted by validate, as in the reference
+    with pytest.raises(ValueError):
+        vb.Matrix(shifted)  # rejected for device use
+    m = vb.Matrix(host)
+    for rhs in (0, 7, 33, 128):
+        with pytest.raises(ValueError):
+            vb.Plan(m, rhs)
+    with pytest.raises(ValueError):
+        vb.Plan(m, 8, "split_row")
+    plan = vb.Plan(m, 32, "auto")
+    assert plan.launch_count() == 1
+    b = torch.zeros(m.scalar_cols * 32, device=DEVICE)
+    with pytest.raises(ValueError):
+        plan.execute(b, torch.zeros(m.scalar_rows * 32 - 1, device=DEVICE))
+    with pytest.raises(ValueError):
+        plan.execute(b.double(), torch.zeros(m.scalar_rows * 32, device=DEVICE))
+    view = m.device_view()
+    assert (view.block_rows, view.block_cols, view.nnzb) == (6, 6, 12)
+    assert (view.scalar_rows, view.scalar_cols) == (host.scalar_rows, host.scalar_cols)
+    m.close()
+
+
+def test_cpp_api_program():
+    """The reference test program restated over the C++ API (tests/cpp/test_api.cpp)."""
+    binary = os.path.join(ROOT, "tests", "cpp", "test_api")
+    note("C++ API program")
+    if not os.path.exists(binary):
+        pytest.fail("tests/cpp/test_api is not built (run __graft_entry__.build())")
+    result = subprocess.run([binary], capture_output=True, text=True, timeout=300)
+    note(result.stdout.strip() + result.stderr.strip())
+    assert result.returncode == 0
+    assert result.stdout.startswith("PASS")

@@ -1,0 +1,136 @@
+"""Host side of the library (no GPU): generate, validate and the test-input
+generator, checked against the oracle bit for bit, plus the C ABI surface."""
+
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle_ffi as o
+import varblockspmm_amd as vb
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def as_oracle(host):
+    return o.HostMatrix(host.block_rows, host.block_cols, **host.arrays())
+
+
+def assert_same_matrix(product, oracle):
+    assert (product.block_rows, product.block_cols) == (oracle.block_rows, oracle.block_cols)
+    for name in o.HostMatrix.FIELDS:
+        np.testing.assert_array_equal(getattr(product, name), getattr(oracle, name), err_msg=name)
+
+
+@pytest.mark.parametrize("distribution", list(vb.DISTRIBUTIONS))
+@pytest.mark.parametrize("locality", list(vb.LOCALITIES))
+@pytest.mark.parametrize("shape", [(9, 17, 4, 11), (33, 20, 16, 12), (25, 25, 1, 13)])
+def test_generate_matches_oracle(distribution, locality, shape):
+    R, C, d, seed = shape
+    product = vb.generate(R, C, d, distribution, locality, seed)
+    oracle = o.generate(R, C, d, distribution, locality, seed)
+    assert_same_matrix(product, oracle)
+
+
+def test_generate_matches_oracle_at_benchmark_size():
+    """BASELINE configuration 2's matrix (1024 rows, degree 8, low variance, random, seed 2)."""
+    assert_same_matrix(vb.generate(1024, 1024, 8, "low", "random", 2), o.generate(1024, 1024, 8, "low", "random", 2))
+
+
+def test_generate_rejects_bad_options():
+    for args in [(0, 4, 1), (4, 0, 1), (4, 4, 0), (4, 4, 17), (4, 3, 4)]:
+        with pytest.raises(ValueError):
+            vb.generate(*args)
+    with pytest.raises(ValueError):
+        vb.generate(4, 4, 1, distribution=9)
+    with pytest.raises(ValueError):
+        vb.generate(4, 4, 1, locality=7)
+
+
+def test_make_random_input_matches_oracle():
+    for count, seed in [(1, 0), (1000, 11), (4097, (1 << 32) + 3)]:
+        np.testing.assert_array_equal(vb.make_random_input(count, seed), o.make_random_input(count, seed))
+
+
+def test_validate_matches_oracle_rule_by_rule():
+    import test_oracle
+
+    base = vb.generate(4, 4, 2, "high", "local", 1)
+    base.validate()
+    for description, mutate, rule in test_oracle.mutations():
+        m = as_oracle(base).copy()
+        mutate(m)
+        product = vb.HostMatrix(m.block_rows, m.block_cols, **{n: getattr(m, n) for n in o.HostMatrix.FIELDS})
+        assert o.validate(m) == rule, description
+        with pytest.raises(ValueError):
+            product.validate()
+
+
+def test_validate_accepts_what_the_reference_accepts():
+    import test_oracle
+
+    m = test_oracle._rows_with_empty()
+    vb.HostMatrix(m.block_rows, m.block_cols, **{n: getattr(m, n) for n in o.HostMatrix.FIELDS}).validate()
+    shifted = vb.generate(6, 6, 2, "high", "random", 3)
+    shifted.row_scalar_off = shifted.row_scalar_off + 8
+    shifted.validate()
+
+
+# ---- the C ABI surface ------------------------------------------------------------------------------
+
+
+def declared_symbols():
+    with open(os.path.join(ROOT, "include", "vbsr.h")) as handle:
+        text = handle.read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(vbsr_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = vb.library()
+    names = declared_symbols()
+    assert len(names) >= 18
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(vb.SIGNATURES)
+
+
+def test_library_links_no_oracle_code():
+    out = subprocess.run(["nm", "-D", "--defined-only", vb.LIBRARY_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    assert "orc_" not in out
+    assert "liboracle" not in subprocess.run(["ldd", vb.LIBRARY_PATH], capture_output=True, text=True).stdout
+
+
+def test_library_holds_gfx950_code_objects():
+    out = subprocess.run(["strings", vb.LIBRARY_PATH], capture_output=True, text=True, check=True).stdout
+    assert "gfx950" in out
+
+
+def test_cpp_api_header_compiles():
+    source = ('#include <varblockspmm/vbsr.hpp>\n'
+              'int main() { vbsr::GeneratorOptions o; o.block_rows = 3; (void)o; return 0; }\n')
+    subprocess.run(["g++", "-std=c++20", "-fsyntax-only", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
+                    "-I" + os.path.join(ROOT, "include"), "-x", "c++", "-"], input=source, text=True, check=True)
+
+
+def test_null_arguments_are_rejected_without_a_gpu():
+    lib = vb.library()
+    assert lib.vbsr_validate(None) == vb.VBSR_INVALID_ARGUMENT
+    assert b"null" in lib.vbsr_last_error()
+    assert lib.vbsr_plan_execute(None, None, None, None) == vb.VBSR_INVALID_ARGUMENT
+    assert lib.vbsr_matrix_device_view(None, None) == vb.VBSR_INVALID_ARGUMENT
+    assert lib.vbsr_plan_launch_count(None) == 0
+    lib.vbsr_matrix_destroy(None)
+    lib.vbsr_plan_destroy(None)
+
+
+def test_launchers_reject_bad_rhs_before_touching_the_gpu():
+    view = vb.DeviceView()
+    view.block_rows = 4
+    for rhs in (0, 7, 12, 128):
+        with pytest.raises(ValueError):
+            vb.launch_row_owned(view, None, None, rhs)
+        with pytest.raises(ValueError):
+            vb.launch_row_owned_scalar(view, None, None, rhs)

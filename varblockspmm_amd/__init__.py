@@ -1,0 +1,300 @@
+"""Python host mirror of the VBSR SpMM library's C ABI (include/vbsr.h).
+
+Names follow the reference C++ API (King-Clawthorne/VarBlockSpMM,
+include/varblockspmm/vbsr.hpp): ``HostMatrix``, ``validate``, ``generate``,
+``Matrix``, ``Plan`` (``execute``, ``launch_count``), ``launch_row_owned`` and
+``launch_row_owned_scalar``.  Errors keep the reference's split:
+``ValueError`` where it throws std::invalid_argument, ``RuntimeError`` where it
+throws std::runtime_error.
+
+Every computation runs in libvarblockspmm_amd.so (HIP kernels for gfx950).
+There is no CPU fallback: importing raises if the library is not built.
+Device buffers and streams are passed as integers (device addresses, stream
+handles) or as torch tensors / torch streams, whose addresses are taken.
+"""
+
+import ctypes
+import os
+
+import numpy as np
+
+PACKAGE_DIR = os.path.dirname(os.path.abspath(__file__))
+LIBRARY_PATH = os.path.join(PACKAGE_DIR, "libvarblockspmm_amd.so")
+
+VBSR_OK, VBSR_INVALID_ARGUMENT, VBSR_RUNTIME_ERROR = 0, 1, 2
+
+DISTRIBUTIONS = {"uniform": 0, "low": 1, "high": 2, "bimodal": 3, "bimodal8or64": 4, "tied8to64": 5}
+LOCALITIES = {"random": 0, "local": 1, "clamped": 2}
+KERNELS = {"auto": 0, "row_owned": 1, "split_row": 2}
+
+_ARRAYS = (("row_ptr", ctypes.c_int32, np.int32), ("block_col", ctypes.c_int32, np.int32),
+           ("row_size", ctypes.c_int32, np.int32), ("col_size", ctypes.c_int32, np.int32),
+           ("row_scalar_off", ctypes.c_int64, np.int64), ("col_scalar_off", ctypes.c_int64, np.int64),
+           ("value_off", ctypes.c_int64, np.int64), ("values", ctypes.c_float, np.float32))
+
+
+class HostView(ctypes.Structure):
+    _fields_ = [("block_rows", ctypes.c_int32), ("block_cols", ctypes.c_int32)] + [
+        item for name, ctype, _ in _ARRAYS
+        for item in ((name, ctypes.POINTER(ctype)), (name + "_len", ctypes.c_int64))]
+
+
+class DeviceView(ctypes.Structure):
+    _fields_ = [("block_rows", ctypes.c_int32), ("block_cols", ctypes.c_int32), ("nnzb", ctypes.c_int32),
+                ("scalar_rows", ctypes.c_int64), ("scalar_cols", ctypes.c_int64),
+                ("row_ptr", ctypes.c_void_p), ("block_col", ctypes.c_void_p), ("row_size", ctypes.c_void_p),
+                ("col_size", ctypes.c_void_p), ("row_scalar_off", ctypes.c_void_p),
+                ("col_scalar_off", ctypes.c_void_p), ("value_off", ctypes.c_void_p), ("values", ctypes.c_void_p)]
+
+
+class GeneratorOptions(ctypes.Structure):
+    _fields_ = [("block_rows", ctypes.c_int32), ("block_cols", ctypes.c_int32), ("degree", ctypes.c_int32),
+                ("rhs_width", ctypes.c_int32), ("distribution", ctypes.c_int32), ("locality", ctypes.c_int32),
+                ("seed", ctypes.c_uint64)]
+
+
+class PlanOptions(ctypes.Structure):
+    _fields_ = [("rhs_width", ctypes.c_int32), ("kernel", ctypes.c_int32)]
+
+
+# Every symbol include/vbsr.h declares, with its ctypes signature.
+_P = ctypes.c_void_p
+SIGNATURES = {
+    "vbsr_last_error": (ctypes.c_char_p, []),
+    "vbsr_validate": (ctypes.c_int, [ctypes.POINTER(HostView)]),
+    "vbsr_generate": (ctypes.c_int, [ctypes.POINTER(GeneratorOptions), ctypes.POINTER(_P)]),
+    "vbsr_host_matrix_view": (ctypes.c_int, [_P, ctypes.POINTER(HostView)]),
+    "vbsr_host_matrix_destroy": (None, [_P]),
+    "vbsr_make_random_input": (ctypes.c_int, [ctypes.c_int64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_float)]),
+    "vbsr_matrix_create": (ctypes.c_int, [ctypes.POINTER(HostView), ctypes.POINTER(_P)]),
+    "vbsr_matrix_destroy": (None, [_P]),
+    "vbsr_matrix_device_view": (ctypes.c_int, [_P, ctypes.POINTER(DeviceView)]),
+    "vbsr_matrix_scalar_rows": (ctypes.c_int64, [_P]),
+    "vbsr_matrix_scalar_cols": (ctypes.c_int64, [_P]),
+    "vbsr_matrix_row_schedule": (ctypes.c_int, [_P, ctypes.POINTER(_P)]),
+    "vbsr_plan_create": (ctypes.c_int, [_P, ctypes.POINTER(PlanOptions), ctypes.POINTER(_P)]),
+    "vbsr_plan_destroy": (None, [_P]),
+    "vbsr_plan_execute": (ctypes.c_int, [_P, _P, _P, _P]),
+    "vbsr_plan_launch_count": (ctypes.c_int, [_P]),
+    "vbsr_launch_row_owned": (ctypes.c_int, [ctypes.POINTER(DeviceView), _P, _P, _P, ctypes.c_int32, _P]),
+    "vbsr_launch_row_owned_scalar": (ctypes.c_int, [ctypes.POINTER(DeviceView), _P, _P, ctypes.c_int32, _P]),
+}
+
+_lib = None
+
+
+def library():
+    """The loaded libvarblockspmm_amd.so; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIBRARY_PATH):
+            raise ImportError(f"{LIBRARY_PATH} is missing: build it with `python -c "
+                              f"'import __graft_entry__ as g; g.build()'` (make -C varblockspmm_amd/csrc)")
+        lib = ctypes.CDLL(LIBRARY_PATH)
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = lib
+    return _lib
+
+
+def _check(status):
+    if status == VBSR_OK:
+        return
+    message = library().vbsr_last_error().decode(errors="replace")
+    if status == VBSR_INVALID_ARGUMENT:
+        raise ValueError(message)
+    raise RuntimeError(message)
+
+
+def _address(obj):
+    """Device address of a torch tensor, or an integer address (0 = null)."""
+    if obj is None:
+        return None
+    if hasattr(obj, "data_ptr"):
+        return obj.data_ptr() or None
+    return int(obj) or None
+
+
+def _check_panel(panel, expected, name):
+    """For torch tensors, checks what the C ABI cannot: dtype, layout, device and size."""
+    if not hasattr(panel, "data_ptr"):
+        return
+    import torch
+    if panel.dtype != torch.float32 or not panel.is_contiguous() or not panel.is_cuda:
+        raise ValueError(f"{name} must be a contiguous float32 device tensor")
+    if panel.numel() != expected:
+        raise ValueError(f"{name} holds {panel.numel()} floats, expected {expected}")
+
+
+def _stream(stream):
+    if stream is None:
+        return None
+    if hasattr(stream, "cuda_stream"):
+        return stream.cuda_stream or None
+    return int(stream) or None
+
+
+class HostMatrix:
+    """Host VBSR matrix with the reference HostMatrix fields (vbsr.hpp:16-29), held as numpy arrays."""
+
+    def __init__(self, block_rows, block_cols, **arrays):
+        self.block_rows = int(block_rows)
+        self.block_cols = int(block_cols)
+        for name, _, dtype in _ARRAYS:
+            setattr(self, name, np.ascontiguousarray(arrays[name], dtype=dtype))
+
+    @property
+    def scalar_rows(self):
+        return int(self.row_scalar_off[-1]) if len(self.row_scalar_off) else 0
+
+    @property
+    def scalar_cols(self):
+        return int(self.col_scalar_off[-1]) if len(self.col_scalar_off) else 0
+
+    @property
+    def nnzb(self):
+        return len(self.block_col)
+
+    def copy(self):
+        return HostMatrix(self.block_rows, self.block_cols, **{n: getattr(self, n).copy() for n, _, _ in _ARRAYS})
+
+    def arrays(self):
+        return {name: getattr(self, name) for name, _, _ in _ARRAYS}
+
+    def _view(self):
+        view = HostView()
+        view.block_rows = self.block_rows
+        view.block_cols = self.block_cols
+        for name, ctype, dtype in _ARRAYS:
+            array = getattr(self, name)
+            if array.dtype != dtype or not array.flags.c_contiguous:
+                array = np.ascontiguousarray(array, dtype=dtype)
+                setattr(self, name, array)
+            setattr(view, name, array.ctypes.data_as(ctypes.POINTER(ctype)))
+            setattr(view, name + "_len", len(array))
+        return view
+
+    def validate(self):
+        """HostMatrix::validate (vbsr.cpp:29-82); raises ValueError."""
+        view = self._view()
+        _check(library().vbsr_validate(ctypes.byref(view)))
+
+
+def validate(matrix):
+    matrix.validate()
+
+
+def generate(block_rows=1024, block_cols=1024, degree=4, distribution="high", locality="local", seed=1,
+             rhs_width=32):
+    """generate (vbsr.hpp:80; generator.cpp:7-88).  distribution: uniform|low|high|bimodal (reference)
+    or bimodal8or64|tied8to64; locality: local (cyclic, reference), random, clamped."""
+    options = GeneratorOptions(block_rows, block_cols, degree, rhs_width,
+                               DISTRIBUTIONS[distribution] if isinstance(distribution, str) else int(distribution),
+                               LOCALITIES[locality] if isinstance(locality, str) else int(locality), seed)
+    lib = library()
+    handle = ctypes.c_void_p()
+    _check(lib.vbsr_generate(ctypes.byref(options), ctypes.byref(handle)))
+    try:
+        view = HostView()
+        _check(lib.vbsr_host_matrix_view(handle, ctypes.byref(view)))
+        arrays = {}
+        for name, _, dtype in _ARRAYS:
+            length = getattr(view, name + "_len")
+            pointer = getattr(view, name)
+            arrays[name] = (np.ctypeslib.as_array(pointer, shape=(length,)).astype(dtype, copy=True)
+                            if length else np.zeros(0, dtype))
+        return HostMatrix(view.block_rows, view.block_cols, **arrays)
+    finally:
+        lib.vbsr_host_matrix_destroy(handle)
+
+
+def make_random_input(count, seed):
+    """The reference test's B (tests/test_main.cpp:42-51) as a float32 numpy array."""
+    out = np.empty(int(count), dtype=np.float32)
+    _check(library().vbsr_make_random_input(int(count), int(seed), out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+    return out
+
+
+class Matrix:
+    """Owning device copy of a validated matrix (reference Matrix, vbsr.hpp:41-64), on the current HIP device."""
+
+    def __init__(self, host):
+        view = host._view()
+        handle = ctypes.c_void_p()
+        _check(library().vbsr_matrix_create(ctypes.byref(view), ctypes.byref(handle)))
+        self._handle = handle
+
+    def close(self):
+        if getattr(self, "_handle", None):
+            library().vbsr_matrix_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def device_view(self):
+        view = DeviceView()
+        _check(library().vbsr_matrix_device_view(self._handle, ctypes.byref(view)))
+        return view
+
+    def row_schedule(self):
+        pointer = ctypes.c_void_p()
+        _check(library().vbsr_matrix_row_schedule(self._handle, ctypes.byref(pointer)))
+        return pointer.value
+
+    @property
+    def scalar_rows(self):
+        return library().vbsr_matrix_scalar_rows(self._handle)
+
+    @property
+    def scalar_cols(self):
+        return library().vbsr_matrix_scalar_cols(self._handle)
+
+
+class Plan:
+    """Reusable execution plan (reference Plan, vbsr.hpp:104-119).  The Matrix must outlive the plan."""
+
+    def __init__(self, matrix, rhs_width=32, kernel="auto"):
+        options = PlanOptions(int(rhs_width), KERNELS[kernel] if isinstance(kernel, str) else int(kernel))
+        handle = ctypes.c_void_p()
+        _check(library().vbsr_plan_create(matrix._handle, ctypes.byref(options), ctypes.byref(handle)))
+        self._handle = handle
+        self._matrix = matrix
+        self.rhs_width = int(rhs_width)
+
+    def close(self):
+        if getattr(self, "_handle", None):
+            library().vbsr_plan_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def execute(self, B, C, stream=None):
+        """Enqueues C = A*B (column-major device buffers) on `stream`; asynchronous."""
+        _check_panel(B, self._matrix.scalar_cols * self.rhs_width, "B")
+        _check_panel(C, self._matrix.scalar_rows * self.rhs_width, "C")
+        _check(library().vbsr_plan_execute(self._handle, _address(B), _address(C), _stream(stream)))
+
+    def launch_count(self):
+        return library().vbsr_plan_launch_count(self._handle)
+
+
+def launch_row_owned(device_view, B, C, rhs, stream=None, row_order=None):
+    """launch_row_owned (vbsr.hpp:158-159): the tuned kernels on a device view."""
+    _check(library().vbsr_launch_row_owned(ctypes.byref(device_view), _address(row_order), _address(B),
+                                           _address(C), int(rhs), _stream(stream)))
+
+
+def launch_row_owned_scalar(device_view, B, C, rhs, stream=None):
+    """launch_row_owned_scalar (vbsr.hpp:161): the reference-order kernel."""
+    _check(library().vbsr_launch_row_owned_scalar(ctypes.byref(device_view), _address(B), _address(C), int(rhs),
+                                                  _stream(stream)))

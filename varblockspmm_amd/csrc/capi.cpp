@@ -1,0 +1,164 @@
+// extern "C" boundary (include/vbsr.h).  Every entry point catches C++
+// exceptions and maps them to status codes: std::invalid_argument ->
+// VBSR_INVALID_ARGUMENT, anything else -> VBSR_RUNTIME_ERROR.  The message is
+// kept per thread for vbsr_last_error().
+#include <exception>
+#include <new>
+
+#include "internal.hpp"
+
+struct vbsr_host_matrix {
+  vbsr_amd::HostMatrix host;
+};
+struct vbsr_matrix {
+  vbsr_amd::DeviceMatrix device;
+  explicit vbsr_matrix(const vbsr_host_view& host) : device(host) {}
+};
+struct vbsr_plan {
+  vbsr_amd::Plan plan;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+template <class F>
+int guarded(F&& body) {
+  try {
+    body();
+    g_last_error.clear();
+    return VBSR_OK;
+  } catch (const std::invalid_argument& e) {
+    g_last_error = e.what();
+    return VBSR_INVALID_ARGUMENT;
+  } catch (const std::bad_alloc&) {
+    g_last_error = "host allocation failed";
+    return VBSR_RUNTIME_ERROR;
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+    return VBSR_RUNTIME_ERROR;
+  } catch (...) {
+    g_last_error = "unknown error";
+    return VBSR_RUNTIME_ERROR;
+  }
+}
+
+template <class T>
+void require(const T* p, const char* name) {
+  if (p == nullptr) throw std::invalid_argument(std::string(name) + " is null");
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* vbsr_last_error(void) { return g_last_error.c_str(); }
+
+int vbsr_validate(const vbsr_host_view* host) {
+  return guarded([&] {
+    require(host, "host");
+    vbsr_amd::validate(*host);
+  });
+}
+
+int vbsr_generate(const vbsr_generator_options* options, vbsr_host_matrix** out) {
+  return guarded([&] {
+    require(options, "options");
+    require(out, "out");
+    *out = nullptr;
+    auto* m = new vbsr_host_matrix{vbsr_amd::generate(*options)};
+    *out = m;
+  });
+}
+
+int vbsr_host_matrix_view(const vbsr_host_matrix* matrix, vbsr_host_view* out) {
+  return guarded([&] {
+    require(matrix, "matrix");
+    require(out, "out");
+    *out = matrix->host.view();
+  });
+}
+
+void vbsr_host_matrix_destroy(vbsr_host_matrix* matrix) { delete matrix; }
+
+int vbsr_make_random_input(int64_t count, uint64_t seed, float* out) {
+  return guarded([&] {
+    if (count < 0) throw std::invalid_argument("negative count");
+    if (count > 0) require(out, "out");
+    vbsr_amd::make_random_input(count, seed, out);
+  });
+}
+
+int vbsr_matrix_create(const vbsr_host_view* host, vbsr_matrix** out) {
+  return guarded([&] {
+    require(host, "host");
+    require(out, "out");
+    *out = nullptr;
+    *out = new vbsr_matrix(*host);
+  });
+}
+
+void vbsr_matrix_destroy(vbsr_matrix* matrix) { delete matrix; }
+
+int vbsr_matrix_device_view(const vbsr_matrix* matrix, vbsr_device_view* out) {
+  return guarded([&] {
+    require(matrix, "matrix");
+    require(out, "out");
+    *out = matrix->device.view();
+  });
+}
+
+int64_t vbsr_matrix_scalar_rows(const vbsr_matrix* matrix) {
+  return matrix ? matrix->device.view().scalar_rows : 0;
+}
+
+int64_t vbsr_matrix_scalar_cols(const vbsr_matrix* matrix) {
+  return matrix ? matrix->device.view().scalar_cols : 0;
+}
+
+int vbsr_matrix_row_schedule(const vbsr_matrix* matrix, const int32_t** row_order) {
+  return guarded([&] {
+    require(matrix, "matrix");
+    require(row_order, "row_order");
+    *row_order = matrix->device.row_order();
+  });
+}
+
+int vbsr_plan_create(const vbsr_matrix* matrix, const vbsr_plan_options* options, vbsr_plan** out) {
+  return guarded([&] {
+    require(matrix, "matrix");
+    require(options, "options");
+    require(out, "out");
+    *out = nullptr;
+    *out = new vbsr_plan{vbsr_amd::Plan(matrix->device, *options)};
+  });
+}
+
+void vbsr_plan_destroy(vbsr_plan* plan) { delete plan; }
+
+int vbsr_plan_execute(const vbsr_plan* plan, const float* B, float* C, hipStream_t stream) {
+  return guarded([&] {
+    require(plan, "plan");
+    plan->plan.execute(B, C, stream);
+  });
+}
+
+int vbsr_plan_launch_count(const vbsr_plan* plan) { return plan ? plan->plan.launch_count() : 0; }
+
+int vbsr_launch_row_owned(const vbsr_device_view* matrix, const int32_t* row_order, const float* B,
+                          float* C, int32_t rhs, hipStream_t stream) {
+  return guarded([&] {
+    require(matrix, "matrix");
+    vbsr_amd::launch_mfma(*matrix, row_order, B, C, rhs, stream);
+  });
+}
+
+int vbsr_launch_row_owned_scalar(const vbsr_device_view* matrix, const float* B, float* C, int32_t rhs,
+                                 hipStream_t stream) {
+  return guarded([&] {
+    require(matrix, "matrix");
+    vbsr_amd::launch_scalar(*matrix, B, C, rhs, stream);
+  });
+}
+
+}  // extern "C"
