@@ -7,8 +7,9 @@ RHS 32, seed 1; A and B values uniform in [-1, 1].  The reference publishes
 (data/publication/regime_map_seed1.csv:362).
 
 Timing: per-step HIP events recorded on the stream the kernel runs on.
-"cold" steps first stream a 1 GiB buffer (untimed) so that neither L2 nor the
-256 MB Infinity Cache holds A, B or C -- inputs are resident in HBM only.
+"cold" steps first read a 1 GiB buffer (untimed, read-only so no dirty lines
+are left behind) so that neither L2 nor the 256 MB Infinity Cache holds A, B
+or C -- inputs are resident in HBM only.
 "hot" steps run back to back, the reference's methodology
 (bench/benchmark.cpp:148-183).  `value` is algorithmic bytes / cold median.
 
@@ -112,7 +113,8 @@ def main():
     stream = torch.cuda.Stream(device=device)
     b_dev = torch.from_numpy(b_host).to(device)
     c_dev = torch.full((host.scalar_rows * args.rhs,), float("nan"), device=device)
-    flush = torch.empty(256 * 1024 * 1024, dtype=torch.float32, device=device)  # 1 GiB
+    flush = torch.ones(256 * 1024 * 1024, dtype=torch.float32, device=device)  # 1 GiB
+    sink = torch.empty((), dtype=torch.float32, device=device)
     torch.cuda.synchronize()
 
     def step():
@@ -136,7 +138,9 @@ def main():
         with torch.cuda.stream(stream):
             for i in range(args.steps):
                 if cold:
-                    flush.add_(1.0)
+                    # Read-only sweep: evicts L2 and the Infinity Cache without
+                    # leaving dirty lines whose write-back would be timed.
+                    torch.sum(flush, (0,), out=sink)
                 starts[i].record(stream)
                 step()
                 ends[i].record(stream)
@@ -223,7 +227,7 @@ def main():
         "data": "synthetic (seeded generator, B = mt19937 uniform[-1,1])",
         "config": {"workload": workload, "kernel": args.kernel, "sum_hw": work["sum_hw"],
                    "algorithmic_bytes": work["bytes"], "flops": work["flops"], "launches": plan.launch_count(),
-                   "timing": "cold = 1 GiB stream between steps (untimed); hot = back to back"},
+                   "timing": "cold = 1 GiB read-only sweep between steps (untimed); hot = back to back"},
         "roofline": {"bound": "hbm" if args.rhs <= 32 else "mfma", "achieved": round(achieved_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "kernel_avg_ms": round(mean, 5)},

@@ -10,8 +10,8 @@
 //    their one-shot helpers) are not provided.
 //  - Distribution gains Bimodal8or64 and Tied8to64; GeneratorOptions gains
 //    clamp_local_columns (clamped instead of cyclic local columns).
-//  - launch_row_owned takes the matrix's row schedule (or nullptr) instead
-//    of the reference's h <= 16 partition counts.
+//  - launch_row_owned takes the matrix's row schedule instead of the
+//    reference's row_shape_order and h <= 16 partition counts.
 #pragma once
 
 #include <cstdint>
@@ -104,11 +104,11 @@ public:
   }
   int64_t scalar_rows() const { return vbsr_matrix_scalar_rows(handle_); }
   int64_t scalar_cols() const { return vbsr_matrix_scalar_cols(handle_); }
-  /** Device permutation of the block rows by decreasing work. */
-  const int32_t* row_schedule() const {
-    const int32_t* order = nullptr;
-    detail::check(vbsr_matrix_row_schedule(handle_, &order));
-    return order;
+  /** The row schedule that Plan passes to launch_row_owned. */
+  vbsr_row_schedule row_schedule() const {
+    vbsr_row_schedule schedule{};
+    detail::check(vbsr_matrix_row_schedule(handle_, &schedule));
+    return schedule;
   }
   const vbsr_matrix* handle() const { return handle_; }
 
@@ -190,9 +190,9 @@ private:
 };
 
 /** The tuned row-owned kernels (reference vbsr.hpp:158-159). */
-inline void launch_row_owned(DeviceMatrix matrix, const int32_t* row_order, const float* B, float* C, int rhs,
-                             hipStream_t stream) {
-  detail::check(vbsr_launch_row_owned(&matrix, row_order, B, C, rhs, stream));
+inline void launch_row_owned(DeviceMatrix matrix, const vbsr_row_schedule& schedule, const float* B, float* C,
+                             int rhs, hipStream_t stream) {
+  detail::check(vbsr_launch_row_owned(&matrix, &schedule, B, C, rhs, stream));
 }
 
 /** The reference-order kernel (reference vbsr.hpp:161). */

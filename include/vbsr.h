@@ -129,11 +129,17 @@ int vbsr_matrix_device_view(const vbsr_matrix* matrix, vbsr_device_view* out);
 /* Matrix::scalar_rows / scalar_cols (vbsr.hpp:52-53). */
 int64_t vbsr_matrix_scalar_rows(const vbsr_matrix* matrix);
 int64_t vbsr_matrix_scalar_cols(const vbsr_matrix* matrix);
-/* The matrix's row schedule: a device permutation of [0, block_rows) that
- * orders block rows by decreasing work (the counterpart of the reference's
- * private row_shape_order, vbsr.cpp:96-102).  Pass it to
- * vbsr_launch_row_owned. */
-int vbsr_matrix_row_schedule(const vbsr_matrix* matrix, const int32_t** row_order);
+/* The matrix's row schedule, built at vbsr_matrix_create: the
+ * counterpart of the reference's private row_shape_order and its small/large
+ * counts (vbsr.cpp:96-102), which Plan passes to launch_row_owned.  Device
+ * arrays owned by the matrix; opaque to callers.  `groups` is the number of
+ * workgroups one launch of the row-owned kernel uses. */
+typedef struct vbsr_row_schedule {
+  const void* rows;   /* device: one 32-byte row item per workgroup */
+  const void* blocks; /* device: one 16-byte descriptor per stored block */
+  int64_t groups;
+} vbsr_row_schedule;
+int vbsr_matrix_row_schedule(const vbsr_matrix* matrix, vbsr_row_schedule* out);
 
 /* Plan(const Matrix&, PlanOptions) (vbsr.hpp:106; plan.cpp:5-18): rejects
  * rhs_width outside {8,16,32,64} and VBSR_KERNEL_SPLIT_ROW.  The plan views
@@ -148,11 +154,13 @@ int vbsr_plan_execute(const vbsr_plan* plan, const float* B, float* C, hipStream
 int vbsr_plan_launch_count(const vbsr_plan* plan);
 
 /* launch_row_owned (vbsr.hpp:158-159; row_owned.cu:397-423): the tuned
- * row-owned kernels for `rhs`.  `row_order` is a device permutation of the
- * block rows (e.g. from vbsr_matrix_row_schedule) or NULL for natural order;
- * it changes only the scheduling, never the result. */
-int vbsr_launch_row_owned(const vbsr_device_view* matrix, const int32_t* row_order, const float* B,
-                          float* C, int32_t rhs, hipStream_t stream);
+ * row-owned kernel for `rhs` over `matrix`, scheduled by `schedule` (from
+ * vbsr_matrix_row_schedule of the matrix that `matrix` views; the reference
+ * passes row_shape_order/small/large in the same role).  B must be 16-byte
+ * aligned (VBSR_INVALID_ARGUMENT otherwise; vbsr_plan_execute accepts any
+ * alignment). */
+int vbsr_launch_row_owned(const vbsr_device_view* matrix, const vbsr_row_schedule* schedule,
+                          const float* B, float* C, int32_t rhs, hipStream_t stream);
 
 /* launch_row_owned_scalar (vbsr.hpp:161; row_owned.cu:376-395): one output
  * per lane, accumulated with fmaf over blocks in row_ptr order and k

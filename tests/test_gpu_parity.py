@@ -163,16 +163,57 @@ def test_order_preserving_kernel_full_size(config):
 
 
 @pytest.mark.parametrize("rhs", [8, 16, 32, 64])
-def test_row_order_changes_no_bits(rhs):
-    note(f"row order rhs={rhs}")
+def test_public_launcher_matches_plan(rhs):
+    """launch_row_owned with the matrix's schedule is exactly Plan::execute."""
+    note(f"launcher rhs={rhs}")
     c = Case(vb.generate(300, 280, 6, "high", "random", 5), rhs, 5)
     view = c.matrix.device_view()
-    scheduled = c.run(lambda: vb.launch_row_owned(view, c.b_dev, c.c_dev, rhs, c.stream, c.matrix.row_schedule()))
-    natural = c.run(lambda: vb.launch_row_owned(view, c.b_dev, c.c_dev, rhs, c.stream, None))
-    np.testing.assert_array_equal(scheduled, natural)
+    launched = c.run(lambda: vb.launch_row_owned(view, c.matrix.row_schedule(), c.b_dev, c.c_dev, rhs, c.stream))
     plan = vb.Plan(c.matrix, rhs)
-    np.testing.assert_array_equal(c.run_plan(plan), scheduled)
-    c.check_tolerance(natural, "natural order")
+    np.testing.assert_array_equal(c.run_plan(plan), launched)
+    c.check_tolerance(launched, "launcher")
+    c.close()
+
+
+@pytest.mark.parametrize("rhs", [8, 32])
+def test_misaligned_b_takes_the_order_preserving_kernel(rhs):
+    """A B panel that is only 4-byte aligned: the tuned launcher refuses it,
+    Plan::execute runs the order-preserving kernel (bit-exact fmaf order)."""
+    note(f"misaligned B rhs={rhs}")
+    c = Case(vb.generate(40, 40, 4, "high", "random", 9), rhs, 9)
+    storage = torch.empty(c.b.size + 4, dtype=torch.float32, device=DEVICE)
+    storage[1:1 + c.b.size].copy_(c.b_dev)
+    shifted = storage[1:1 + c.b.size]
+    assert shifted.data_ptr() % 16 != 0
+    view = c.matrix.device_view()
+    with pytest.raises(ValueError):
+        vb.launch_row_owned(view, c.matrix.row_schedule(), shifted, c.c_dev, rhs, c.stream)
+    plan = vb.Plan(c.matrix, rhs)
+    result = c.run(lambda: plan.execute(shifted, c.c_dev, c.stream))
+    np.testing.assert_array_equal(result, o.fmaf_order(c.oracle, c.b, rhs))
+    c.close()
+
+
+@pytest.mark.parametrize("rhs", [8, 16, 32, 64])
+def test_infinite_b_matches_reference_semantics(rhs):
+    """+Inf in one B entry: every output whose row touches it with a positive A
+    value is +Inf, never NaN (padding lanes must not form 0 * Inf)."""
+    note(f"inf B rhs={rhs}")
+    host = hand_made([8, 24, 40, 56], [8, 24, 40], [[0, 1, 2], [2, 0], [1], [0, 2]], seed=4)
+    values = np.abs(host.values) + 0.5  # strictly positive A
+    host = vb.HostMatrix(host.block_rows, host.block_cols, **{**host.arrays(), "values": values})
+    c = Case(host, rhs, 31)
+    b = np.abs(c.b).reshape(rhs, host.scalar_cols)
+    b[:, host.col_scalar_off[0] + 5] = np.inf  # last k of a half step of the 8-wide column 0
+    b[:, host.col_scalar_off[2] + 37] = np.inf  # inside the half step of the 40-wide column 2
+    c.b = b.reshape(-1).copy()
+    c.b_dev = torch.from_numpy(c.b).to(DEVICE)
+    result = c.run_plan(vb.Plan(c.matrix, rhs)).reshape(rhs, host.scalar_rows)
+    expected = o.cpu_reference(c.oracle, c.b, rhs).reshape(rhs, host.scalar_rows)
+    assert not np.any(np.isnan(result))
+    np.testing.assert_array_equal(np.isinf(result), np.isinf(expected))
+    finite = np.isfinite(expected)
+    np.testing.assert_allclose(result[finite], expected[finite], rtol=1e-5, atol=1e-5)
     c.close()
 
 

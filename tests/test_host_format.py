@@ -131,6 +131,6 @@ def test_launchers_reject_bad_rhs_before_touching_the_gpu():
     view.block_rows = 4
     for rhs in (0, 7, 12, 128):
         with pytest.raises(ValueError):
-            vb.launch_row_owned(view, None, None, rhs)
+            vb.launch_row_owned(view, vb.RowSchedule(), None, None, rhs)
         with pytest.raises(ValueError):
             vb.launch_row_owned_scalar(view, None, None, rhs)

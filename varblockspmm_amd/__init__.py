@@ -53,6 +53,10 @@ class GeneratorOptions(ctypes.Structure):
                 ("seed", ctypes.c_uint64)]
 
 
+class RowSchedule(ctypes.Structure):
+    _fields_ = [("rows", ctypes.c_void_p), ("blocks", ctypes.c_void_p), ("groups", ctypes.c_int64)]
+
+
 class PlanOptions(ctypes.Structure):
     _fields_ = [("rhs_width", ctypes.c_int32), ("kernel", ctypes.c_int32)]
 
@@ -71,12 +75,13 @@ SIGNATURES = {
     "vbsr_matrix_device_view": (ctypes.c_int, [_P, ctypes.POINTER(DeviceView)]),
     "vbsr_matrix_scalar_rows": (ctypes.c_int64, [_P]),
     "vbsr_matrix_scalar_cols": (ctypes.c_int64, [_P]),
-    "vbsr_matrix_row_schedule": (ctypes.c_int, [_P, ctypes.POINTER(_P)]),
+    "vbsr_matrix_row_schedule": (ctypes.c_int, [_P, ctypes.POINTER(RowSchedule)]),
     "vbsr_plan_create": (ctypes.c_int, [_P, ctypes.POINTER(PlanOptions), ctypes.POINTER(_P)]),
     "vbsr_plan_destroy": (None, [_P]),
     "vbsr_plan_execute": (ctypes.c_int, [_P, _P, _P, _P]),
     "vbsr_plan_launch_count": (ctypes.c_int, [_P]),
-    "vbsr_launch_row_owned": (ctypes.c_int, [ctypes.POINTER(DeviceView), _P, _P, _P, ctypes.c_int32, _P]),
+    "vbsr_launch_row_owned": (ctypes.c_int, [ctypes.POINTER(DeviceView), ctypes.POINTER(RowSchedule), _P, _P,
+                                             ctypes.c_int32, _P]),
     "vbsr_launch_row_owned_scalar": (ctypes.c_int, [ctypes.POINTER(DeviceView), _P, _P, ctypes.c_int32, _P]),
 }
 
@@ -243,9 +248,10 @@ class Matrix:
         return view
 
     def row_schedule(self):
-        pointer = ctypes.c_void_p()
-        _check(library().vbsr_matrix_row_schedule(self._handle, ctypes.byref(pointer)))
-        return pointer.value
+        """The row schedule Plan passes to launch_row_owned (a RowSchedule)."""
+        schedule = RowSchedule()
+        _check(library().vbsr_matrix_row_schedule(self._handle, ctypes.byref(schedule)))
+        return schedule
 
     @property
     def scalar_rows(self):
@@ -288,9 +294,9 @@ class Plan:
         return library().vbsr_plan_launch_count(self._handle)
 
 
-def launch_row_owned(device_view, B, C, rhs, stream=None, row_order=None):
-    """launch_row_owned (vbsr.hpp:158-159): the tuned kernels on a device view."""
-    _check(library().vbsr_launch_row_owned(ctypes.byref(device_view), _address(row_order), _address(B),
+def launch_row_owned(device_view, schedule, B, C, rhs, stream=None):
+    """launch_row_owned (vbsr.hpp:158-159): the tuned kernel on a device view with its matrix's schedule."""
+    _check(library().vbsr_launch_row_owned(ctypes.byref(device_view), ctypes.byref(schedule), _address(B),
                                            _address(C), int(rhs), _stream(stream)))
 
 

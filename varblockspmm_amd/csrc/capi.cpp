@@ -116,11 +116,11 @@ int64_t vbsr_matrix_scalar_cols(const vbsr_matrix* matrix) {
   return matrix ? matrix->device.view().scalar_cols : 0;
 }
 
-int vbsr_matrix_row_schedule(const vbsr_matrix* matrix, const int32_t** row_order) {
+int vbsr_matrix_row_schedule(const vbsr_matrix* matrix, vbsr_row_schedule* out) {
   return guarded([&] {
     require(matrix, "matrix");
-    require(row_order, "row_order");
-    *row_order = matrix->device.row_order();
+    require(out, "out");
+    *out = matrix->device.schedule();
   });
 }
 
@@ -145,11 +145,12 @@ int vbsr_plan_execute(const vbsr_plan* plan, const float* B, float* C, hipStream
 
 int vbsr_plan_launch_count(const vbsr_plan* plan) { return plan ? plan->plan.launch_count() : 0; }
 
-int vbsr_launch_row_owned(const vbsr_device_view* matrix, const int32_t* row_order, const float* B,
-                          float* C, int32_t rhs, hipStream_t stream) {
+int vbsr_launch_row_owned(const vbsr_device_view* matrix, const vbsr_row_schedule* schedule,
+                          const float* B, float* C, int32_t rhs, hipStream_t stream) {
   return guarded([&] {
     require(matrix, "matrix");
-    vbsr_amd::launch_mfma(*matrix, row_order, B, C, rhs, stream);
+    require(schedule, "schedule");
+    vbsr_amd::launch_row_owned(*matrix, *schedule, B, C, rhs, stream);
   });
 }
 

@@ -35,6 +35,43 @@ HostMatrix generate(const vbsr_generator_options& options);
 // make_random_input (tests/test_main.cpp:42-51).
 void make_random_input(int64_t count, uint64_t seed, float* out);
 
+// ---- row schedule (schedule.cpp) -------------------------------------------
+
+// XCDs of an MI355X.  Workgroups are dispatched to XCDs round-robin by index.
+constexpr int kXcds = 8;
+
+// One workgroup's work: block row `row` (all of its rows and blocks).  A
+// padding slot has nblocks < 0.  32 bytes, read with one scalar load.
+struct alignas(16) RowItem {
+  int64_t c_off;    // row_scalar_off[row]: first row of C written
+  int32_t first;    // row_ptr[row]
+  int32_t nblocks;  // row_ptr[row + 1] - row_ptr[row]; < 0 for a padding slot
+  int32_t h;        // row_size[row]: leading dimension of the row's blocks
+  int32_t row;      // block row (diagnostics only)
+  int32_t pad0, pad1;
+};
+static_assert(sizeof(RowItem) == 32, "RowItem is read as 8 dwords");
+
+// Per stored block, in row_ptr order: where its payload starts in `values`
+// and where its B slice starts, with the block width in the top byte.
+struct alignas(16) BlockDesc {
+  int64_t a_off;  // value_off[blk]
+  int64_t b_off;  // col_scalar_off[block_col[blk]] | int64(w) << 56
+};
+static_assert(sizeof(BlockDesc) == 16, "BlockDesc is read as one dwordx4");
+constexpr int kWidthShift = 56;
+
+struct HostSchedule {
+  std::vector<RowItem> rows;      // one per workgroup, in launch order
+  std::vector<BlockDesc> blocks;  // one per stored block
+  int64_t groups{};               // workgroups to launch (multiple of kXcds)
+};
+
+// Orders the block rows for one launch: each XCD gets a contiguous band of
+// block rows (its B slices stay in that XCD's L2 when columns are local),
+// heaviest rows first within a band.  Deterministic.
+HostSchedule build_schedule(const vbsr_host_view& host);
+
 // ---- device format (device_matrix.cpp) ----------------------------------
 
 // Matrix (vbsr.hpp:41-64): owns device copies of every array plus the row
@@ -47,18 +84,14 @@ public:
   DeviceMatrix& operator=(const DeviceMatrix&) = delete;
 
   const vbsr_device_view& view() const { return view_; }
-  const int32_t* row_order() const { return row_order_; }
+  const vbsr_row_schedule& schedule() const { return schedule_; }
 
 private:
   vbsr_device_view view_{};
-  int32_t* row_order_{};
+  vbsr_row_schedule schedule_{};
   std::vector<void*> allocations_;
   void release() noexcept;
 };
-
-// Host-side construction of the row schedule: block rows sorted by decreasing
-// estimated work (ties keep ascending row index).
-std::vector<int32_t> build_row_schedule(const vbsr_host_view& host);
 
 // ---- kernels -------------------------------------------------------------
 
@@ -68,15 +101,18 @@ inline bool supported_rhs(int rhs) { return rhs == 8 || rhs == 16 || rhs == 32 |
 // Order-preserving kernel (row_owned_scalar.hip).
 void launch_scalar(const vbsr_device_view& a, const float* b, float* c, int rhs, hipStream_t stream);
 
-// MFMA row-owned kernels (row_owned_mfma.hip).  Launch count: 1.
-void launch_mfma(const vbsr_device_view& a, const int32_t* row_order, const float* b, float* c,
-                 int rhs, hipStream_t stream);
+// Row-owned MFMA kernel (row_owned_mfma.hip).  Launch count: 1 (0 for an
+// empty schedule).  Requires row_owned_supported(a, b): B 16-byte aligned and
+// fewer than 2^26 scalar columns (32-bit buffer offsets).
+bool row_owned_supported(const vbsr_device_view& a, const float* b);
+void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& schedule, const float* b, float* c,
+                      int rhs, hipStream_t stream);
 
 // ---- plan (plan.cpp) -------------------------------------------------------
 
 struct Plan {
   vbsr_device_view a{};
-  const int32_t* row_order{};
+  vbsr_row_schedule schedule{};
   vbsr_plan_options options{};
   Plan(const DeviceMatrix& matrix, const vbsr_plan_options& options);
   void execute(const float* b, float* c, hipStream_t stream) const;

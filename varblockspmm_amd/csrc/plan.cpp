@@ -2,16 +2,21 @@
 //
 // The reference splits RHS-32 rows at h <= 16 into two CUDA launches and
 // picks a different CUDA kernel per width (row_owned.cu:333-358, 397-423).
-// On MI355X every width runs one launch of the MFMA row-owned kernel: one
-// wave64 owns one block row at a time and covers the row's h x rhs output in
-// 16x16 MFMA tiles, so the row-height split has no counterpart; the block
-// rows are ordered by decreasing work at Matrix construction instead.
+// On MI355X every width runs one launch of the row-owned MFMA kernel: a
+// workgroup owns a block row, its four waves share the row's k steps and
+// reduce their partial tiles in LDS, so the row height no longer decides the
+// kernel and the height split has no counterpart.  The matrix's row schedule
+// (schedule.cpp) orders and places the rows instead.
+//
+// B panels that are not 16-byte aligned (the kernel's vector loads need it),
+// and matrices with 2^26 or more scalar columns (its 32-bit buffer offsets),
+// go to the order-preserving kernel, which has neither limit.
 #include "internal.hpp"
 
 namespace vbsr_amd {
 
 Plan::Plan(const DeviceMatrix& matrix, const vbsr_plan_options& o)
-    : a(matrix.view()), row_order(matrix.row_order()), options(o) {
+    : a(matrix.view()), schedule(matrix.schedule()), options(o) {
   if (!supported_rhs(o.rhs_width)) throw std::invalid_argument("rhs_width must be 8,16,32,64");
   if (o.kernel == VBSR_KERNEL_SPLIT_ROW)
     throw std::invalid_argument("split-row is reserved and not provided; use RowOwned");
@@ -20,9 +25,12 @@ Plan::Plan(const DeviceMatrix& matrix, const vbsr_plan_options& o)
 }
 
 void Plan::execute(const float* b, float* c, hipStream_t stream) const {
-  launch_mfma(a, row_order, b, c, options.rhs_width, stream);
+  if (row_owned_supported(a, b))
+    launch_row_owned(a, schedule, b, c, options.rhs_width, stream);
+  else
+    launch_scalar(a, b, c, options.rhs_width, stream);
 }
 
-int Plan::launch_count() const { return a.block_rows > 0 ? 1 : 0; }
+int Plan::launch_count() const { return schedule.groups > 0 ? 1 : 0; }
 
 }  // namespace vbsr_amd
