@@ -132,12 +132,12 @@ int64_t vbsr_matrix_scalar_cols(const vbsr_matrix* matrix);
 /* The matrix's row schedule, built at vbsr_matrix_create: the
  * counterpart of the reference's private row_shape_order and its small/large
  * counts (vbsr.cpp:96-102), which Plan passes to launch_row_owned.  Device
- * arrays owned by the matrix; opaque to callers.  `groups` is the number of
- * workgroups one launch of the row-owned kernel uses. */
+ * arrays owned by the matrix; opaque to callers. */
 typedef struct vbsr_row_schedule {
+  const void* steps;  /* device: one 16-byte record per k step */
   const void* rows;   /* device: one 32-byte row item per workgroup */
-  const void* blocks; /* device: one 16-byte descriptor per stored block */
-  int64_t groups;
+  int64_t groups;     /* workgroups of one launch */
+  int32_t step_limit; /* index of the last step record */
 } vbsr_row_schedule;
 int vbsr_matrix_row_schedule(const vbsr_matrix* matrix, vbsr_row_schedule* out);
 

@@ -241,6 +241,10 @@ EDGE_MATRICES = {
     "all-64": lambda: hand_made([64] * 12, [64] * 12, [[(i * 5 + j) % 12 for j in range(4)] for i in range(12)]),
     "narrow-wide": lambda: hand_made([8, 64] * 8, [64, 8] * 8, [[j for j in range(16) if (i + j) % 3 == 0]
                                                                  for i in range(16)]),
+    # 100 blocks of width 64 in one row: 400 k steps, more than one workgroup
+    # segment holds (256), so the row is accumulated across segments
+    "long-row": lambda: hand_made([16, 40, 8], [64] * 100 + [8] * 20,
+                                  [list(range(100)), list(range(0, 120, 3)), list(range(100, 120))]),
 }
 
 

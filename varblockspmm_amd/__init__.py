@@ -54,7 +54,8 @@ class GeneratorOptions(ctypes.Structure):
 
 
 class RowSchedule(ctypes.Structure):
-    _fields_ = [("rows", ctypes.c_void_p), ("blocks", ctypes.c_void_p), ("groups", ctypes.c_int64)]
+    _fields_ = [("steps", ctypes.c_void_p), ("rows", ctypes.c_void_p), ("groups", ctypes.c_int64),
+                ("step_limit", ctypes.c_int32)]
 
 
 class PlanOptions(ctypes.Structure):

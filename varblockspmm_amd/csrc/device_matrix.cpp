@@ -54,9 +54,10 @@ DeviceMatrix::DeviceMatrix(const vbsr_host_view& host) {
     view_.col_scalar_off = upload(host.col_scalar_off, host.col_scalar_off_len, allocations_);
     view_.value_off = upload(host.value_off, host.value_off_len, allocations_);
     view_.values = upload(host.values, host.values_len, allocations_);
+    schedule_.steps = upload(schedule.steps.data(), int64_t(schedule.steps.size()), allocations_);
     schedule_.rows = upload(schedule.rows.data(), int64_t(schedule.rows.size()), allocations_);
-    schedule_.blocks = upload(schedule.blocks.data(), int64_t(schedule.blocks.size()), allocations_);
     schedule_.groups = schedule.groups;
+    schedule_.step_limit = int32_t(std::max<size_t>(schedule.steps.size(), 1) - 1);
   } catch (...) {
     release();
     throw;

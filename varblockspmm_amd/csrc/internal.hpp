@@ -40,36 +40,37 @@ void make_random_input(int64_t count, uint64_t seed, float* out);
 // XCDs of an MI355X.  Workgroups are dispatched to XCDs round-robin by index.
 constexpr int kXcds = 8;
 
-// One workgroup's work: block row `row` (all of its rows and blocks).  A
-// padding slot has nblocks < 0.  32 bytes, read with one scalar load.
+// One k step of one block row: 16 columns of one block, or the 8 columns
+// that end a block whose width is 8 mod 16 (a half step).
+struct alignas(16) StepRec {
+  int64_t a_off;  // value_off[blk] + k0 * h: first value of the step's columns
+  int64_t b_off;  // col_scalar_off[block_col[blk]] + k0, | kHalfStep for a half step
+};
+static_assert(sizeof(StepRec) == 16, "StepRec is read as one dwordx4");
+constexpr int64_t kHalfStep = int64_t(1) << 62;
+
+// One workgroup's work: block row `row`, whose steps are
+// steps[step_first .. step_first + step_count).  A padding slot has
+// step_count < 0.  32 bytes, read with one scalar load.
 struct alignas(16) RowItem {
-  int64_t c_off;    // row_scalar_off[row]: first row of C written
-  int32_t first;    // row_ptr[row]
-  int32_t nblocks;  // row_ptr[row + 1] - row_ptr[row]; < 0 for a padding slot
-  int32_t h;        // row_size[row]: leading dimension of the row's blocks
-  int32_t row;      // block row (diagnostics only)
+  int64_t c_off;       // row_scalar_off[row]: first row of C written
+  int32_t step_first;  // index of the row's first StepRec
+  int32_t step_count;  // the row's k steps; < 0 for a padding slot
+  int32_t h;           // row_size[row]: leading dimension of the row's blocks
+  int32_t row;         // block row (diagnostics only)
   int32_t pad0, pad1;
 };
 static_assert(sizeof(RowItem) == 32, "RowItem is read as 8 dwords");
 
-// Per stored block, in row_ptr order: where its payload starts in `values`
-// and where its B slice starts, with the block width in the top byte.
-struct alignas(16) BlockDesc {
-  int64_t a_off;  // value_off[blk]
-  int64_t b_off;  // col_scalar_off[block_col[blk]] | int64(w) << 56
-};
-static_assert(sizeof(BlockDesc) == 16, "BlockDesc is read as one dwordx4");
-constexpr int kWidthShift = 56;
-
 struct HostSchedule {
-  std::vector<RowItem> rows;      // one per workgroup, in launch order
-  std::vector<BlockDesc> blocks;  // one per stored block
-  int64_t groups{};               // workgroups to launch (multiple of kXcds)
+  std::vector<StepRec> steps;  // row after row, blocks in row_ptr order
+  std::vector<RowItem> rows;   // one per workgroup, in launch order
+  int64_t groups{};            // workgroups of one launch (multiple of kXcds)
 };
 
-// Orders the block rows for one launch: each XCD gets a contiguous band of
-// block rows (its B slices stay in that XCD's L2 when columns are local),
-// heaviest rows first within a band.  Deterministic.
+// Step records plus the launch order of the block rows: each XCD gets a
+// contiguous band of block rows (its B slices stay in that XCD's L2 when
+// columns are local), heaviest rows first within a band.  Deterministic.
 HostSchedule build_schedule(const vbsr_host_view& host);
 
 // ---- device format (device_matrix.cpp) ----------------------------------
@@ -92,6 +93,7 @@ private:
   std::vector<void*> allocations_;
   void release() noexcept;
 };
+
 
 // ---- kernels -------------------------------------------------------------
 

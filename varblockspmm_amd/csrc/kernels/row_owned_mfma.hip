@@ -4,19 +4,18 @@
 //
 // Work unit.  One workgroup (4 waves) owns one block row of height h and
 // writes its h x RHS slab of C; nothing else writes it, so there are no
-// atomics and no global workspace.  The row's k steps (16 k of one block, or
-// the 8 k that end a block whose width is 8 mod 16) are dealt to the four
-// waves in runs of kRun consecutive steps; each wave accumulates all T =
-// ceil(h/16) row tiles for its steps, and the four partial slabs are summed
-// in LDS in a fixed order, (w0 + w2) + (w1 + w3).  Every A line and every B
-// line of the row is therefore requested by one wave only, with both halves
-// of each 128-byte line in adjacent loads, and the accumulation order depends
-// only on the matrix, so results are bit-identical from run to run.
+// atomics and no global workspace.  The row's k steps (16 columns of one
+// block, or the 8 that end a block whose width is 8 mod 16; one precomputed
+// record each) are dealt to the four waves in runs of two; each wave
+// accumulates all T = ceil(h/16) row tiles for its steps, and the four
+// partial slabs are summed in LDS in a fixed order, (w0 + w2) + (w1 + w3).
+// The accumulation order depends only on the matrix, so results are
+// bit-identical from run to run.
 //
 // Arithmetic.  v_mfma_f32_16x16x4_f32 on transposed 16x16 output tiles,
 //   D[n][r] = sum_k B[k, n0 + n] * A[16t + r, k],
-// lane 16*g + x supplies src0 = B[k, n0 + x] and src1 = A[16t + x, k] for the
-// k that lane group g holds, and result register v of lane 16*g + x is
+// lane 16*g + x supplies src0 = B[k, n0 + x] and src1 = A[16t + x, k] with
+// k = k0 + 4*g + i for MFMA i, and result register v of lane 16*g + x is
 // C[16t + x, n0 + 4*g + v]: 16 lanes store 64 consecutive bytes of a C column.
 // Output column r of a tile depends only on src1 lanes with x == r, and
 // output row n only on src0 lanes with x == n, so lanes beyond the last
@@ -24,31 +23,31 @@
 // their results are never stored.  They load duplicate in-bounds addresses
 // instead of branching.
 //
-// k steps.  Every step loads, per lane and tile, A[r, k0 + 4*j + i]
-// (i = 0..3) and one 16-byte B[k0 + 4*j .. k0 + 4*j + 3, n] per 16-column
-// RHS tile, with j = g for a full step and j = g & 1 for a half step; MFMA i
-// takes element i.  In a half step lane groups 2-3 repeat the k of groups
-// 0-1 and are dead: they feed 0 * 0, so each k enters once and non-finite
-// inputs reach C exactly as in the reference.  Every step issues the same
-// loads and MFMAs, so the loop has no branch but its back edge.
+// Memory.  A and B are read with raw buffer loads whose resources cover
+// exactly one step: 16 (or 8) columns of the block, and the step's k range
+// of each B column.  Lanes that must contribute nothing get zeros from the
+// hardware range check instead of from extra instructions: in a half step
+// lane groups 2-3 address columns 8-15 of A, past the 8-column resource, and
+// the B lanes holding k0 + 8 .. k0 + 15 use an offset past every resource;
+// a step beyond a wave's last one gets zero-byte resources.  Those lanes
+// therefore feed 0 * 0, so each k enters once and non-finite inputs reach C
+// exactly as in the reference.
 //
-// Memory.  A and B are read with raw buffer loads: per block, one buffer
-// resource for the block payload (exact byte bounds) and one per RHS tile for
-// the B slice; the k offset of A rides in the scalar offset.  Loads run
-// kDepth - 1 steps ahead of the MFMAs through a register ring; past a wave's
-// last step the ring re-loads that step, whose lanes are all dead.  Block
-// descriptors are read once per chunk of 64 blocks (lane j holds block j) and
-// broadcast with v_readlane.
+// A is loaded straight into MFMA layout: each 16-lane quarter of a load reads
+// 64 contiguous bytes of one block column.  B is not: in MFMA layout a quarter
+// would touch 16 columns, 16 bytes each, and the vector L1 processes each
+// piece as a separate access.  So B is loaded four lanes per column (each
+// quarter reads 64 contiguous bytes of four columns), written to the wave's
+// LDS slot and read back in MFMA layout; the slot is XOR-swizzled so that
+// both the 16-byte writes and reads are free of bank conflicts.
+//
+// Pipeline.  A wave's step records are read with one load (lane j holds its
+// j-th step).  Two register stages alternate: the loads of step j + 1 are in
+// flight while step j computes.  All lane offsets are per-row constants, so
+// a step costs its loads, its buffer resources, one select and its MFMAs.
 #include <hip/hip_runtime.h>
 
 #include "../internal.hpp"
-
-#ifndef VBSR_RING_DEPTH
-#define VBSR_RING_DEPTH 2
-#endif
-#ifndef VBSR_STEP_RUN
-#define VBSR_STEP_RUN 2
-#endif
 
 namespace vbsr_amd {
 namespace {
@@ -60,13 +59,15 @@ constexpr int kWave = 64;
 constexpr int kWaves = 4;
 constexpr int kThreads = kWave * kWaves;
 constexpr int kMaxTiles = 4;  // h <= 64
-constexpr int kDepth = VBSR_RING_DEPTH;
-constexpr int kRun = VBSR_STEP_RUN;
-constexpr int64_t kOffsetMask = (int64_t(1) << kWidthShift) - 1;
+constexpr int kRun = 2;       // consecutive steps dealt to one wave
+// Steps whose records one wave holds at once (one per lane): a row is
+// processed in segments of kWaves * kWave steps.
+constexpr int kSegment = kWaves * kWave;
+constexpr int64_t kOffsetMask = kHalfStep - 1;
 // Buffer resource word 3 for raw (unformatted, unswizzled) dword access.
 constexpr int kRawBufferFlags = 0x00020000;
-static_assert(kDepth >= 1 && kDepth <= 6, "ring depth");
-static_assert(kRun >= 1, "step run");
+// A buffer offset past the end of every resource: its loads return zeros.
+constexpr uint32_t kOutOfRange = 0xfffffff0u;
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
@@ -85,53 +86,86 @@ constexpr int rhs_tiles() {
   return RHS < 16 ? 1 : RHS / 16;
 }
 
-template <int RHS, int T>
-struct Step {
-  float a[T][4];
-  f32x4 b[rhs_tiles<RHS>()];
-  bool half;
-};
-
+// LDS of one workgroup: each wave's B slot, and two slots for the partial
+// slabs of the reduction.
 template <int RHS>
 struct Shared {
+  f32x4 b_slot[kWaves][rhs_tiles<RHS>()][kWave];
   f32x4 partial[2][kMaxTiles * rhs_tiles<RHS>()][kWave];
 };
 
-// The steps of one chunk owned by `wave`: runs r = wave, wave + 4, ... of kRun
+// Position, within a wave's 1 KB B slot of one RHS tile, of the 16 bytes
+// B[k0 + 4q .. k0 + 4q + 3, n0 + n]: column-major with the four 16-byte
+// pieces of column n permuted by an XOR of n's bits 1-2.  Writers (lane
+// 4n + q) and readers (lane 16q + n) then each cover all banks.
+__device__ __forceinline__ int b_slot_index(int n, int q) {
+  return n * 4 + ((q ^ (n >> 1) ^ (n >> 2)) & 3);
+}
+
+// Steps of a segment dealt to `wave`: runs r = wave, wave + 4, ... of kRun
 // steps each, the last run possibly short.
-__device__ __forceinline__ int owned_steps(int steps, int wave) {
-  const int full = steps / kRun;
-  const int rest = steps % kRun;
+__device__ __forceinline__ int owned_steps(int count, int wave) {
+  const int full = count / kRun;
+  const int rest = count % kRun;
   const int full_owned = full > wave ? (full - wave + kWaves - 1) / kWaves : 0;
   return full_owned * kRun + ((rest > 0 && full % kWaves == wave) ? rest : 0);
 }
 
+// Index within its segment of the wave's j-th step.
+__device__ __forceinline__ int owned_step(int j, int wave) {
+  return ((j / kRun) * kWaves + wave) * kRun + j % kRun;
+}
+
+// One step's operands as loaded.
 template <int RHS, int T>
-__device__ __forceinline__ void row_body(const vbsr_device_view& a, const RowItem& item, const BlockDesc* blocks,
-                                         const float* b, float* c, Shared<RHS>& shared, int wave, int lane) {
+struct Stage {
+  float a[T][4];
+  f32x4 b[rhs_tiles<RHS>()];
+};
+
+struct Launch {
+  vbsr_device_view a;
+  const StepRec* steps;
+  const RowItem* rows;
+  int32_t step_limit;  // index of the last StepRec
+  const float* b;
+  float* c;
+};
+
+template <int RHS, int T>
+__device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, Shared<RHS>& shared, int wave,
+                                         int lane) {
   constexpr int kRhsTiles = rhs_tiles<RHS>();
   constexpr int kRhsLanes = RHS < 16 ? RHS : 16;
   const int group = lane >> 4;
   const int x = lane & 15;
-  const bool upper = group >= 2;
   const int h = uniform(item.h);
-  const int nblocks = uniform(item.nblocks);
-  const int first = uniform(item.first);
+  const int count = uniform(item.step_count);
+  const int first = uniform(item.step_first);
   const int last_rows = h - 16 * (T - 1);  // 8 or 16
-  const uint32_t ldb = uint32_t(a.scalar_cols);
+  const uint32_t ldb = uint32_t(L.a.scalar_cols);
 
-  // Per-lane byte offsets.  Rows past h and rhs columns past RHS read a
-  // duplicate in-bounds address.
-  uint32_t a_row[T];
+  // A lane offsets (bytes from the step's first value): row 16t + x of column
+  // 4g.  Rows past h read a duplicate row.
+  uint32_t a_lane[T];
 #pragma unroll
-  for (int t = 0; t < T; ++t) a_row[t] = uint32_t(16 * t + (t == T - 1 ? (x & (last_rows - 1)) : x)) * 4u;
-  const uint32_t a_full = uint32_t(4 * group * h) * 4u;
-  const uint32_t a_half = uint32_t(4 * (group & 1) * h) * 4u;
-  const uint32_t b_row = uint32_t(x & (kRhsLanes - 1)) * ldb * 4u;
-  const uint32_t b_full = uint32_t(4 * group) * 4u;
-  const uint32_t b_half = uint32_t(4 * (group & 1)) * 4u;
-  const uint32_t a_stride = uint32_t(h) * 4u;                   // bytes between columns of a block
-  const uint32_t b_span = (uint32_t(kRhsLanes - 1) * ldb) * 4u;  // bytes of a B tile past its first column
+  for (int t = 0; t < T; ++t)
+    a_lane[t] = uint32_t(16 * t + (t == T - 1 ? (x & (last_rows - 1)) : x)) * 4u + uint32_t(group * 16 * h);
+  const int a_stride = h * 4;  // bytes between block columns
+  const uint32_t a_full_bytes = uint32_t(16 * h) * 4u;
+  const uint32_t a_half_bytes = uint32_t(8 * h) * 4u;
+
+  // B load layout: lane 4n + q reads B[k0 + 4q .. k0 + 4q + 3, n0 + n] (rhs
+  // columns past RHS read a duplicate column; in a half step q = 2, 3 read
+  // nothing).
+  const int b_n = lane >> 2;
+  const int b_q = lane & 3;
+  const uint32_t b_full = uint32_t(b_n & (kRhsLanes - 1)) * ldb * 4u + uint32_t(16 * b_q);
+  const uint32_t b_half = b_q < 2 ? b_full : kOutOfRange;
+  const uint32_t b_span = uint32_t(kRhsLanes - 1) * ldb * 4u;  // a B tile's bytes before its last column
+  const int slot_write = b_slot_index(b_n, b_q);
+  const int slot_read = b_slot_index(x, group);
+  f32x4(&slot)[kRhsTiles][kWave] = shared.b_slot[wave];
 
   f32x4 acc[T][kRhsTiles];
 #pragma unroll
@@ -139,90 +173,67 @@ __device__ __forceinline__ void row_body(const vbsr_device_view& a, const RowIte
 #pragma unroll
     for (int nt = 0; nt < kRhsTiles; ++nt) acc[t][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  for (int chunk = 0; chunk < nblocks; chunk += kWave) {
-    const int count = min(kWave, nblocks - chunk);
-    const BlockDesc desc = blocks[first + chunk + min(lane, count - 1)];
-    const int w_lane = int(uint64_t(desc.b_off) >> kWidthShift);
-    int steps = 0;
-    for (int j = 0; j < count; ++j) steps += (__builtin_amdgcn_readlane(w_lane, j) + 8) >> 4;
-    const int mine = owned_steps(steps, wave);
+  for (int seg = 0; seg < count; seg += kSegment) {
+    const int seg_count = min(kSegment, count - seg);
+    const int mine = owned_steps(seg_count, wave);
     if (mine == 0) continue;
+    const StepRec rec = L.steps[min(first + seg + owned_step(min(lane, mine - 1), wave), L.step_limit)];
 
-    // Load stream: global step `s` = block `lb` at k offset `lk`.
-    int s = 0, lb = 0, lk = 0, w = 0, issued = 0;
-    rsrc_t a_rsrc;
-    rsrc_t b_rsrc[kRhsTiles];
-    auto enter_block = [&](int blk) {
-      const int64_t a_off = lane_value(desc.a_off, blk);
-      const int64_t bw = lane_value(desc.b_off, blk);
-      w = int(bw >> kWidthShift);
-      a_rsrc = make_rsrc(a.values + a_off, uint32_t(h * w) * 4u);
-      const float* b_base = b + (bw & kOffsetMask);
-#pragma unroll
-      for (int nt = 0; nt < kRhsTiles; ++nt)
-        b_rsrc[nt] = make_rsrc(b_base + int64_t(nt) * 16 * ldb, b_span + uint32_t(w) * 4u);
-    };
-    auto next_step = [&]() {
-      lk += (w - lk) == 8 ? 8 : 16;
-      if (lk >= w) {
-        lk = 0;
-        enter_block(++lb);
-      }
-      ++s;
-    };
-    enter_block(0);
-    while ((s / kRun) % kWaves != wave) next_step();
-
-    Step<RHS, T> ring[kDepth];
-    auto issue = [&](Step<RHS, T>& st) {
-      const bool half = (w - lk) == 8;
-      const uint32_t va = half ? a_half : a_full;
-      const uint32_t vb = b_row + (half ? b_half : b_full);
-      const int ka = lk * int(a_stride);
+    // Loads the wave's j-th step of the segment; a dead step (live == false)
+    // gets zero-byte resources.
+    auto issue = [&](Stage<RHS, T>& st, int j, bool live) {
+      const int l = min(j, kWave - 1);
+      const int64_t a_off = lane_value(rec.a_off, l);
+      const int64_t b_word = lane_value(rec.b_off, l);
+      const bool half = (b_word & kHalfStep) != 0;
+      const rsrc_t a_rsrc = make_rsrc(L.a.values + a_off, live ? (half ? a_half_bytes : a_full_bytes) : 0u);
       // The buffer-load builtins return raw bits (u32 / u32x4): bit-cast them.
 #pragma unroll
       for (int t = 0; t < T; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          st.a[t][i] = __builtin_bit_cast(
-              float, __builtin_amdgcn_raw_buffer_load_b32(a_rsrc, int(a_row[t] + va), ka + i * int(a_stride), 0));
+          st.a[t][i] =
+              __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(a_rsrc, int(a_lane[t]), i * a_stride, 0));
+      const uint32_t vb = half ? b_half : b_full;
+      const uint32_t b_bytes = live ? b_span + (half ? 32u : 64u) : 0u;
+      const float* b_base = L.b + (b_word & kOffsetMask);
 #pragma unroll
-      for (int nt = 0; nt < kRhsTiles; ++nt)
-        st.b[nt] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc[nt], int(vb), lk * 4, 0));
-      st.half = half;
-      if (issued + 1 < mine) {
-        ++issued;
-        do next_step();
-        while ((s / kRun) % kWaves != wave);
+      for (int nt = 0; nt < kRhsTiles; ++nt) {
+        const rsrc_t b_rsrc = make_rsrc(b_base + int64_t(nt) * 16 * ldb, b_bytes);
+        st.b[nt] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, int(vb), 0, 0));
       }
     };
-    // Branch-free: a dead lane feeds 0 * 0 and every step runs the same MFMAs.
-    auto compute = [&](const Step<RHS, T>& st, bool live) {
-      const bool dead = !live || (st.half && upper);
+    // Moves B through the LDS slot into MFMA layout, then runs the step.
+    auto compute = [&](const Stage<RHS, T>& st) {
+#pragma unroll
+      for (int nt = 0; nt < kRhsTiles; ++nt) slot[nt][slot_write] = st.b[nt];
       f32x4 bv[kRhsTiles];
 #pragma unroll
-      for (int nt = 0; nt < kRhsTiles; ++nt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) bv[nt][i] = dead ? 0.0f : st.b[nt][i];
+      for (int nt = 0; nt < kRhsTiles; ++nt) bv[nt] = slot[nt][slot_read];
 #pragma unroll
       for (int t = 0; t < T; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float av = dead ? 0.0f : st.a[t][i];
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
           for (int nt = 0; nt < kRhsTiles; ++nt)
-            acc[t][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[nt][i], av, acc[t][nt], 0, 0, 0);
-        }
+            acc[t][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[nt][i], st.a[t][i], acc[t][nt], 0, 0, 0);
     };
 
-#pragma unroll
-    for (int k = 0; k < kDepth - 1; ++k) issue(ring[k]);
-    for (int j = 0; j < mine; j += kDepth) {
-#pragma unroll
-      for (int u = 0; u < kDepth; ++u) {
-        issue(ring[(u + kDepth - 1) % kDepth]);
-        compute(ring[u], j + u < mine);
-      }
+    // Two stages: step j + 1 loads while step j computes.  The loop has one
+    // exit, at its back edge, so the compiler keeps the accumulators in
+    // place; with runs of two steps only a wave holding a short final run
+    // has an odd count, and its last compute multiplies a dead step's zeros.
+    // A scheduling barrier after each issue keeps the compiler from moving
+    // the prefetch below the compute it must overlap.
+    Stage<RHS, T> r0, r1;
+    issue(r0, 0, true);
+    for (int j = 0; j < mine; j += 2) {
+      issue(r1, j + 1, j + 1 < mine);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(r0);
+      issue(r0, j + 2, j + 2 < mine);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(r1);
     }
   }
 
@@ -249,8 +260,8 @@ __device__ __forceinline__ void row_body(const vbsr_device_view& a, const RowIte
   }
   __syncthreads();
   if (wave != 0) return;
-  const int64_t ldc = a.scalar_rows;
-  float* c_row = c + item.c_off + x;
+  const int64_t ldc = L.a.scalar_rows;
+  float* c_row = L.c + item.c_off + x;
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     if (t < T - 1 || x < last_rows) {
@@ -268,32 +279,30 @@ __device__ __forceinline__ void row_body(const vbsr_device_view& a, const RowIte
 }
 
 template <int RHS>
-__global__ __launch_bounds__(kThreads) void row_owned_mfma_kernel(vbsr_device_view a, const RowItem* __restrict__ rows,
-                                                                  const BlockDesc* __restrict__ blocks,
-                                                                  const float* __restrict__ b, float* __restrict__ c) {
+__global__ __launch_bounds__(kThreads) void row_owned_mfma_kernel(Launch L) {
   __shared__ Shared<RHS> shared;
   const int wave = uniform(int(threadIdx.x) / kWave);
   const int lane = int(threadIdx.x) % kWave;
-  const RowItem item = rows[blockIdx.x];
-  if (uniform(item.nblocks) < 0) return;  // padding slot: the whole workgroup leaves
+  const RowItem item = L.rows[blockIdx.x];
+  if (uniform(item.step_count) < 0) return;  // padding slot: the whole workgroup leaves
   switch ((uniform(item.h) + 15) >> 4) {
-  case 1: row_body<RHS, 1>(a, item, blocks, b, c, shared, wave, lane); break;
-  case 2: row_body<RHS, 2>(a, item, blocks, b, c, shared, wave, lane); break;
-  case 3: row_body<RHS, 3>(a, item, blocks, b, c, shared, wave, lane); break;
-  default: row_body<RHS, 4>(a, item, blocks, b, c, shared, wave, lane); break;
+  case 1: row_body<RHS, 1>(L, item, shared, wave, lane); break;
+  case 2: row_body<RHS, 2>(L, item, shared, wave, lane); break;
+  case 3: row_body<RHS, 3>(L, item, shared, wave, lane); break;
+  default: row_body<RHS, 4>(L, item, shared, wave, lane); break;
   }
 }
 
 template <int RHS>
-void launch(const vbsr_device_view& a, const vbsr_row_schedule& s, const float* b, float* c, hipStream_t stream) {
-  row_owned_mfma_kernel<RHS><<<dim3(unsigned(s.groups)), dim3(kThreads), 0, stream>>>(
-      a, static_cast<const RowItem*>(s.rows), static_cast<const BlockDesc*>(s.blocks), b, c);
+void launch(const Launch& L, int64_t groups, hipStream_t stream) {
+  row_owned_mfma_kernel<RHS><<<dim3(unsigned(groups)), dim3(kThreads), 0, stream>>>(L);
 }
 
 }  // namespace
 
 bool row_owned_supported(const vbsr_device_view& a, const float* b) {
-  // 32-bit buffer offsets: a B tile spans 15 columns of ld K plus one block.
+  // 32-bit buffer offsets: a B tile spans 15 columns of ld K plus one step,
+  // and must stay below the out-of-range offset.
   return reinterpret_cast<uintptr_t>(b) % 16 == 0 && a.scalar_cols < (int64_t(1) << 26);
 }
 
@@ -304,11 +313,12 @@ void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& s, con
     throw std::invalid_argument("row-owned kernel needs a 16-byte aligned B and fewer than 2^26 scalar columns");
   if (s.groups <= 0) return;
   if (s.groups > int64_t(0x7fffffff)) throw std::invalid_argument("schedule too large for one launch");
+  const Launch L{a, static_cast<const StepRec*>(s.steps), static_cast<const RowItem*>(s.rows), s.step_limit, b, c};
   switch (rhs) {
-  case 8: launch<8>(a, s, b, c, stream); break;
-  case 16: launch<16>(a, s, b, c, stream); break;
-  case 32: launch<32>(a, s, b, c, stream); break;
-  default: launch<64>(a, s, b, c, stream); break;
+  case 8: launch<8>(L, s.groups, stream); break;
+  case 16: launch<16>(L, s.groups, stream); break;
+  case 32: launch<32>(L, s.groups, stream); break;
+  default: launch<64>(L, s.groups, stream); break;
   }
   check_hip(hipGetLastError(), "row_owned_mfma launch");
 }
