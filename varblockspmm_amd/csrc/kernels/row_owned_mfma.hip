@@ -20,31 +20,33 @@
 // Output column r of a tile depends only on src1 lanes with x == r, and
 // output row n only on src0 lanes with x == n, so lanes beyond the last
 // tile's rows (h = 8, 24, 40, 56) or beyond RHS (rhs 8) may hold any value:
-// their results are never stored.  They load duplicate in-bounds addresses
-// instead of branching.
+// their results are never stored.
 //
 // Memory.  A and B are read with raw buffer loads whose resources cover
-// exactly one step: 16 (or 8) columns of the block, and the step's k range
-// of each B column.  Lanes that must contribute nothing get zeros from the
-// hardware range check instead of from extra instructions: in a half step
-// lane groups 2-3 address columns 8-15 of A, past the 8-column resource, and
-// the B lanes holding k0 + 8 .. k0 + 15 use an offset past every resource;
-// a step beyond a wave's last one gets zero-byte resources.  Those lanes
-// therefore feed 0 * 0, so each k enters once and non-finite inputs reach C
-// exactly as in the reference.
+// exactly one step: the step's 16 (or 8) columns of the block, and the
+// step's k range of each B column.  Lanes that must contribute nothing get
+// zeros from the hardware range check instead of from extra instructions:
+// in a half step A columns 8-15 lie past the 8-column resource and the B
+// lanes holding k0 + 8 .. k0 + 15 use an offset past every resource; a step
+// beyond a wave's last one gets zero-byte resources.  Those lanes therefore
+// feed 0 * 0, so each k enters once and non-finite inputs reach C exactly as
+// in the reference.
 //
-// A is loaded straight into MFMA layout: each 16-lane quarter of a load reads
-// 64 contiguous bytes of one block column.  B is not: in MFMA layout a quarter
-// would touch 16 columns, 16 bytes each, and the vector L1 processes each
-// piece as a separate access.  So B is loaded four lanes per column (each
-// quarter reads 64 contiguous bytes of four columns), written to the wave's
-// LDS slot and read back in MFMA layout; the slot is XOR-swizzled so that
-// both the 16-byte writes and reads are free of bank conflicts.
+// A step's A tile is 16 contiguous block columns (64 h bytes).  It is read
+// whole, 16 bytes per lane and 1 KB per load, with the non-temporal hint:
+// every load covers whole 128-byte lines, and A, which is read exactly once,
+// does not displace B from L2.  The tile goes through the wave's LDS slot,
+// stored column-major with a leading dimension of 16 T + 4 floats so that the
+// MFMA-layout reads hit 64 distinct banks.  B is loaded four lanes per column
+// (each quarter reads 64 contiguous bytes of four columns), written to the
+// wave's B slot and read back in MFMA layout; that slot is XOR-swizzled so
+// that both the 16-byte writes and reads are free of bank conflicts.
 //
 // Pipeline.  A wave's step records are read with one load (lane j holds its
 // j-th step).  Two register stages alternate: the loads of step j + 1 are in
 // flight while step j computes.  All lane offsets are per-row constants, so
-// a step costs its loads, its buffer resources, one select and its MFMAs.
+// a step costs its loads, its buffer resources, its LDS round trip and its
+// MFMAs.
 #include <hip/hip_runtime.h>
 
 #include "../internal.hpp"
@@ -68,6 +70,8 @@ constexpr int64_t kOffsetMask = kHalfStep - 1;
 constexpr int kRawBufferFlags = 0x00020000;
 // A buffer offset past the end of every resource: its loads return zeros.
 constexpr uint32_t kOutOfRange = 0xfffffff0u;
+// Cache policy of the A loads: non-temporal (streamed, read once).
+constexpr int kNonTemporal = 2;
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
@@ -86,12 +90,20 @@ constexpr int rhs_tiles() {
   return RHS < 16 ? 1 : RHS / 16;
 }
 
-// LDS of one workgroup: each wave's B slot, and two slots for the partial
-// slabs of the reduction.
+// LDS of one workgroup: one area per wave holding its B slot and its A slot.
+// The reduction's two partial slabs reuse the areas of waves 2 and 3 (whose
+// main loops are over by then), which are sized for them.
 template <int RHS>
-struct Shared {
-  f32x4 b_slot[kWaves][rhs_tiles<RHS>()][kWave];
-  f32x4 partial[2][kMaxTiles * rhs_tiles<RHS>()][kWave];
+struct Lds {
+  static constexpr int kBBytes = rhs_tiles<RHS>() * kWave * 16;
+  static constexpr int kABytes = 16 * (16 * kMaxTiles + 4) * 4;
+  static constexpr int kSlotBytes = kBBytes + kABytes;
+  static constexpr int kPartialBytes = kMaxTiles * rhs_tiles<RHS>() * kWave * 16;
+  static constexpr int kBigBytes = kSlotBytes > kPartialBytes ? kSlotBytes : kPartialBytes;
+  static constexpr int kTotal = 2 * kSlotBytes + 2 * kBigBytes;
+  static __device__ __forceinline__ int area(int wave) {
+    return wave < 2 ? wave * kSlotBytes : 2 * kSlotBytes + (wave - 2) * kBigBytes;
+  }
 };
 
 // Position, within a wave's 1 KB B slot of one RHS tile, of the 16 bytes
@@ -116,10 +128,11 @@ __device__ __forceinline__ int owned_step(int j, int wave) {
   return ((j / kRun) * kWaves + wave) * kRun + j % kRun;
 }
 
-// One step's operands as loaded.
+// One step's operands as loaded: A load q holds floats 256 q + 4 lane .. + 3
+// of the step's column-major tile.
 template <int RHS, int T>
 struct Stage {
-  float a[T][4];
+  f32x4 a[T];
   f32x4 b[rhs_tiles<RHS>()];
 };
 
@@ -133,10 +146,11 @@ struct Launch {
 };
 
 template <int RHS, int T>
-__device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, Shared<RHS>& shared, int wave,
-                                         int lane) {
+__device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, char* lds, int wave, int lane) {
+  using Layout = Lds<RHS>;
   constexpr int kRhsTiles = rhs_tiles<RHS>();
   constexpr int kRhsLanes = RHS < 16 ? RHS : 16;
+  constexpr int ld = 16 * T + 4;  // A slot: float (r, k) of the step at k * ld + r
   const int group = lane >> 4;
   const int x = lane & 15;
   const int h = uniform(item.h);
@@ -145,13 +159,24 @@ __device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, S
   const int last_rows = h - 16 * (T - 1);  // 8 or 16
   const uint32_t ldb = uint32_t(L.a.scalar_cols);
 
-  // A lane offsets (bytes from the step's first value): row 16t + x of column
-  // 4g.  Rows past h read a duplicate row.
-  uint32_t a_lane[T];
+  char* area = lds + Layout::area(wave);
+  f32x4* b_slot = reinterpret_cast<f32x4*>(area);
+  float* a_slot = reinterpret_cast<float*>(area + Layout::kBBytes);
+
+  // A slot positions of this lane's loaded floats.  Lanes past the tile
+  // (h = 8 mod 16) hold zeros and write them to the slot's padding (rows
+  // 16 T .. 16 T + 3 of column lane & 15), which is never read.
+  int a_write[T];
 #pragma unroll
-  for (int t = 0; t < T; ++t)
-    a_lane[t] = uint32_t(16 * t + (t == T - 1 ? (x & (last_rows - 1)) : x)) * 4u + uint32_t(group * 16 * h);
-  const int a_stride = h * 4;  // bytes between block columns
+  for (int q = 0; q < T; ++q) {
+    const int f = 256 * q + 4 * lane;
+    const int k = f / h;
+    a_write[q] = f < 16 * h ? k * ld + (f - k * h) : (lane & 15) * ld + 16 * T;
+  }
+  // MFMA-layout reads: row 16 t + x of column 4 g + i; rows past h read a
+  // duplicate row.
+  const int a_read = 4 * group * ld + x;
+  const int a_read_last = 4 * group * ld + 16 * (T - 1) + (x & (last_rows - 1));
   const uint32_t a_full_bytes = uint32_t(16 * h) * 4u;
   const uint32_t a_half_bytes = uint32_t(8 * h) * 4u;
 
@@ -165,7 +190,6 @@ __device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, S
   const uint32_t b_span = uint32_t(kRhsLanes - 1) * ldb * 4u;  // a B tile's bytes before its last column
   const int slot_write = b_slot_index(b_n, b_q);
   const int slot_read = b_slot_index(x, group);
-  f32x4(&slot)[kRhsTiles][kWave] = shared.b_slot[wave];
 
   f32x4 acc[T][kRhsTiles];
 #pragma unroll
@@ -187,13 +211,11 @@ __device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, S
       const int64_t b_word = lane_value(rec.b_off, l);
       const bool half = (b_word & kHalfStep) != 0;
       const rsrc_t a_rsrc = make_rsrc(L.a.values + a_off, live ? (half ? a_half_bytes : a_full_bytes) : 0u);
-      // The buffer-load builtins return raw bits (u32 / u32x4): bit-cast them.
+      // The buffer-load builtins return raw bits (u32x4): bit-cast them.
 #pragma unroll
-      for (int t = 0; t < T; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          st.a[t][i] =
-              __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(a_rsrc, int(a_lane[t]), i * a_stride, 0));
+      for (int q = 0; q < T; ++q)
+        st.a[q] = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, 16 * lane + 1024 * q, 0, kNonTemporal));
       const uint32_t vb = half ? b_half : b_full;
       const uint32_t b_bytes = live ? b_span + (half ? 32u : 64u) : 0u;
       const float* b_base = L.b + (b_word & kOffsetMask);
@@ -203,20 +225,25 @@ __device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, S
         st.b[nt] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, int(vb), 0, 0));
       }
     };
-    // Moves B through the LDS slot into MFMA layout, then runs the step.
+    // Moves A and B through the wave's LDS slots into MFMA layout, then runs
+    // the step.
     auto compute = [&](const Stage<RHS, T>& st) {
 #pragma unroll
-      for (int nt = 0; nt < kRhsTiles; ++nt) slot[nt][slot_write] = st.b[nt];
+      for (int q = 0; q < T; ++q) *reinterpret_cast<f32x4*>(a_slot + a_write[q]) = st.a[q];
+#pragma unroll
+      for (int nt = 0; nt < kRhsTiles; ++nt) b_slot[nt * kWave + slot_write] = st.b[nt];
       f32x4 bv[kRhsTiles];
 #pragma unroll
-      for (int nt = 0; nt < kRhsTiles; ++nt) bv[nt] = slot[nt][slot_read];
+      for (int nt = 0; nt < kRhsTiles; ++nt) bv[nt] = b_slot[nt * kWave + slot_read];
 #pragma unroll
       for (int t = 0; t < T; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i) {
+          const float av = t < T - 1 ? a_slot[a_read + 16 * t + i * ld] : a_slot[a_read_last + i * ld];
 #pragma unroll
           for (int nt = 0; nt < kRhsTiles; ++nt)
-            acc[t][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[nt][i], st.a[t][i], acc[t][nt], 0, 0, 0);
+            acc[t][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[nt][i], av, acc[t][nt], 0, 0, 0);
+        }
     };
 
     // Two stages: step j + 1 loads while step j computes.  The loop has one
@@ -237,26 +264,31 @@ __device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, S
     }
   }
 
-  // Fixed-order reduction of the four partial slabs: (w0 + w2) + (w1 + w3).
+  // Fixed-order reduction of the four partial slabs, (w0 + w2) + (w1 + w3),
+  // through the LDS areas of waves 2 and 3.
+  f32x4* part2 = reinterpret_cast<f32x4*>(lds + Layout::area(2));
+  f32x4* part3 = reinterpret_cast<f32x4*>(lds + Layout::area(3));
   if (wave >= 2) {
+    f32x4* part = wave == 2 ? part2 : part3;
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
-      for (int nt = 0; nt < kRhsTiles; ++nt) shared.partial[wave - 2][t * kRhsTiles + nt][lane] = acc[t][nt];
+      for (int nt = 0; nt < kRhsTiles; ++nt) part[(t * kRhsTiles + nt) * kWave + lane] = acc[t][nt];
   }
   __syncthreads();
   if (wave < 2) {
+    const f32x4* part = wave == 0 ? part2 : part3;
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
-      for (int nt = 0; nt < kRhsTiles; ++nt) acc[t][nt] += shared.partial[wave][t * kRhsTiles + nt][lane];
+      for (int nt = 0; nt < kRhsTiles; ++nt) acc[t][nt] += part[(t * kRhsTiles + nt) * kWave + lane];
   }
   __syncthreads();
   if (wave == 1) {
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
-      for (int nt = 0; nt < kRhsTiles; ++nt) shared.partial[0][t * kRhsTiles + nt][lane] = acc[t][nt];
+      for (int nt = 0; nt < kRhsTiles; ++nt) part2[(t * kRhsTiles + nt) * kWave + lane] = acc[t][nt];
   }
   __syncthreads();
   if (wave != 0) return;
@@ -267,7 +299,7 @@ __device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, S
     if (t < T - 1 || x < last_rows) {
 #pragma unroll
       for (int nt = 0; nt < kRhsTiles; ++nt) {
-        const f32x4 sum = acc[t][nt] + shared.partial[0][t * kRhsTiles + nt][lane];
+        const f32x4 sum = acc[t][nt] + part2[(t * kRhsTiles + nt) * kWave + lane];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int n = nt * 16 + 4 * group + v;
@@ -280,16 +312,16 @@ __device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, S
 
 template <int RHS>
 __global__ __launch_bounds__(kThreads) void row_owned_mfma_kernel(Launch L) {
-  __shared__ Shared<RHS> shared;
+  __shared__ __attribute__((aligned(16))) char lds[Lds<RHS>::kTotal];
   const int wave = uniform(int(threadIdx.x) / kWave);
   const int lane = int(threadIdx.x) % kWave;
   const RowItem item = L.rows[blockIdx.x];
   if (uniform(item.step_count) < 0) return;  // padding slot: the whole workgroup leaves
   switch ((uniform(item.h) + 15) >> 4) {
-  case 1: row_body<RHS, 1>(L, item, shared, wave, lane); break;
-  case 2: row_body<RHS, 2>(L, item, shared, wave, lane); break;
-  case 3: row_body<RHS, 3>(L, item, shared, wave, lane); break;
-  default: row_body<RHS, 4>(L, item, shared, wave, lane); break;
+  case 1: row_body<RHS, 1>(L, item, lds, wave, lane); break;
+  case 2: row_body<RHS, 2>(L, item, lds, wave, lane); break;
+  case 3: row_body<RHS, 3>(L, item, lds, wave, lane); break;
+  default: row_body<RHS, 4>(L, item, lds, wave, lane); break;
   }
 }
 
