@@ -6,7 +6,11 @@ RHS 32, seed 1; A and B values uniform in [-1, 1].  The reference publishes
 0.95043 ms median for this exact instance on an RTX 5060 Ti
 (data/publication/regime_map_seed1.csv:362).
 
-Timing: per-step HIP events recorded on the stream the kernel runs on.
+Timing: per-step HIP events recorded on the stream the kernel runs on, created
+with hipEventDisableSystemFence: the HIP runtime's timing-only events, which
+skip the system-scope cache writeback/invalidate that a default event adds
+around the kernel (the runtime documents them as the accurate way to time on
+AMD GPUs).  The median of default events is reported beside it.
 "cold" steps first read a 1 GiB buffer (untimed, read-only so no dirty lines
 are left behind) so that neither L2 nor the 256 MB Infinity Cache holds A, B
 or C -- inputs are resident in HBM only.
@@ -20,6 +24,7 @@ Prints one JSON line.  Single GPU only: --gpus N > 1 exits with a message.
 """
 
 import argparse
+import ctypes
 import json
 import os
 import platform
@@ -63,6 +68,52 @@ def algorithmic_work(host, rhs):
     meta = 4 * (R + 1) + 4 * nnzb + 4 * R + 4 * C + 8 * (R + 1) + 8 * (C + 1) + 8 * (nnzb + 1)
     return {"sum_hw": S, "bytes": 4 * S + 4 * rhs * K + 4 * rhs * M + meta, "flops": 2.0 * rhs * S,
             "scalar_rows": M, "scalar_cols": K, "nnzb": nnzb}
+
+
+HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000
+
+
+class TimingEvents:
+    """hipEventDisableSystemFence events from the HIP runtime instance torch
+    loaded (found by path, so that its stream handles are valid here)."""
+
+    def __init__(self):
+        path = None
+        with open("/proc/self/maps") as maps:
+            for line in maps:
+                if "libamdhip64" in line:
+                    path = line.split()[-1]
+                    break
+        if path is None:
+            raise RuntimeError("the HIP runtime is not loaded")
+        self.hip = ctypes.CDLL(path)
+        self.hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.events = []
+
+    def create(self):
+        event = ctypes.c_void_p()
+        if self.hip.hipEventCreateWithFlags(ctypes.byref(event), HIP_EVENT_DISABLE_SYSTEM_FENCE) != 0:
+            raise RuntimeError("hipEventCreateWithFlags failed")
+        self.events.append(event)
+        return event
+
+    def record(self, event, stream):
+        if self.hip.hipEventRecord(event, ctypes.c_void_p(stream.cuda_stream)) != 0:
+            raise RuntimeError("hipEventRecord failed")
+
+    def elapsed_ms(self, start, end):
+        ms = ctypes.c_float()
+        if self.hip.hipEventElapsedTime(ctypes.byref(ms), start, end) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def close(self):
+        for event in self.events:
+            self.hip.hipEventDestroy(event)
+        self.events = []
 
 
 def percentile_95(sorted_values):
@@ -130,9 +181,19 @@ def main():
     first_result = c_dev.cpu().numpy().copy()
     print("[bench] warmup done", file=sys.stderr, flush=True)
 
-    def timed(cold):
-        starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-        ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    timing = TimingEvents()
+
+    def timed(cold, fenced=False):
+        if fenced:  # default events (system-scope fence around the kernel)
+            starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+            ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+            record = lambda event: event.record(stream)
+            elapsed = lambda start, end: start.elapsed_time(end)
+        else:
+            starts = [timing.create() for _ in range(args.steps)]
+            ends = [timing.create() for _ in range(args.steps)]
+            record = lambda event: timing.record(event, stream)
+            elapsed = timing.elapsed_ms
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         with torch.cuda.stream(stream):
@@ -141,17 +202,19 @@ def main():
                     # Read-only sweep: evicts L2 and the Infinity Cache without
                     # leaving dirty lines whose write-back would be timed.
                     torch.sum(flush, (0,), out=sink)
-                starts[i].record(stream)
+                record(starts[i])
                 step()
-                ends[i].record(stream)
+                record(ends[i])
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        return sorted(s.elapsed_time(e) for s, e in zip(starts, ends)), wall
+        return sorted(elapsed(s, e) for s, e in zip(starts, ends)), wall
 
     cold_ms, cold_wall = timed(True)
     print("[bench] cold steps done", file=sys.stderr, flush=True)
     hot_ms, hot_wall = timed(False)
     print("[bench] hot steps done", file=sys.stderr, flush=True)
+    fenced_ms, _ = timed(True, fenced=True)
+    timing.close()
     final_result = c_dev.cpu().numpy()
     bit_stable = bool(np.array_equal(first_result.view(np.uint32), final_result.view(np.uint32)))
 
@@ -217,6 +280,7 @@ def main():
         "p95_ms": round(percentile_95(cold_ms), 5),
         "hot_median_ms": round(hot_median, 5),
         "hot_p95_ms": round(percentile_95(hot_ms), 5),
+        "default_event_median_ms": round(fenced_ms[len(fenced_ms) // 2], 5),
         "gflops": round(gflops, 1),
         "hbm_roofline_frac": round(value_gbs / HBM_PEAK_GBS, 4),
         "fp32_roofline_frac": round(gflops / 1e3 / FP32_PEAK_TFLOPS, 4),
@@ -227,7 +291,9 @@ def main():
         "data": "synthetic (seeded generator, B = mt19937 uniform[-1,1])",
         "config": {"workload": workload, "kernel": args.kernel, "sum_hw": work["sum_hw"],
                    "algorithmic_bytes": work["bytes"], "flops": work["flops"], "launches": plan.launch_count(),
-                   "timing": "cold = 1 GiB read-only sweep between steps (untimed); hot = back to back"},
+                   "timing": "hipEventDisableSystemFence events on the kernel's stream; cold = 1 GiB read-only "
+                             "sweep between steps (untimed); hot = back to back; default_event_median_ms = cold "
+                             "median with default (system-fenced) events"},
         "roofline": {"bound": "hbm" if args.rhs <= 32 else "mfma", "achieved": round(achieved_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "kernel_avg_ms": round(mean, 5)},
