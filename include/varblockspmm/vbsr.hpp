@@ -6,8 +6,9 @@
 // Differences from the reference header:
 //  - cpu_reference is not part of the library.  It is the test oracle and
 //    lives in oracle/vbsr_oracle.h (orc_cpu_reference).
-//  - The two vendor-library baselines (ScalarCsrPlan, GroupedGemmPlan and
-//    their one-shot helpers) are not provided.
+//  - ScalarCsrPlan runs on rocSPARSE instead of cuSPARSE.  GroupedGemmPlan
+//    (the cuBLAS grouped-GEMM baseline) and the one-shot baseline helpers
+//    are not provided.
 //  - Distribution gains Bimodal8or64 and Tied8to64; GeneratorOptions gains
 //    clamp_local_columns (clamped instead of cyclic local columns).
 //  - launch_row_owned takes the matrix's row schedule instead of the
@@ -187,6 +188,32 @@ public:
 
 private:
   std::shared_ptr<vbsr_plan> plan_;
+};
+
+/** Persistent rocSPARSE baseline on an expanded scalar CSR copy of the
+ * matrix (reference ScalarCsrPlan, vbsr.hpp:121-136).  Not thread-safe. */
+class ScalarCsrPlan {
+public:
+  ScalarCsrPlan(const HostMatrix& matrix, int rhs_width) {
+    const vbsr_host_view v = matrix.view();
+    vbsr_csr_plan* handle = nullptr;
+    detail::check(vbsr_csr_plan_create(&v, rhs_width, &handle));
+    plan_.reset(handle);
+  }
+  ScalarCsrPlan(const ScalarCsrPlan&) = delete;
+  ScalarCsrPlan& operator=(const ScalarCsrPlan&) = delete;
+  /** Enqueues the baseline multiplication on `stream`. */
+  void execute(const float* B, float* C, hipStream_t stream = 0) {
+    detail::check(vbsr_csr_plan_execute(plan_.get(), B, C, stream));
+  }
+  /** Returns persistent temporary storage allocated after the first execution. */
+  size_t workspace_bytes() const { return size_t(vbsr_csr_plan_workspace_bytes(plan_.get())); }
+
+private:
+  struct Destroy {
+    void operator()(vbsr_csr_plan* p) const { vbsr_csr_plan_destroy(p); }
+  };
+  std::unique_ptr<vbsr_csr_plan, Destroy> plan_;
 };
 
 /** The tuned row-owned kernels (reference vbsr.hpp:158-159). */

@@ -169,6 +169,24 @@ int vbsr_launch_row_owned(const vbsr_device_view* matrix, const vbsr_row_schedul
 int vbsr_launch_row_owned_scalar(const vbsr_device_view* matrix, const float* B, float* C,
                                  int32_t rhs, hipStream_t stream);
 
+/* ScalarCsrPlan (vbsr.hpp:121-136; cusparse_baseline.cu:35-188): the
+ * library baseline, on rocSPARSE.  vbsr_csr_plan_create validates the host
+ * matrix (and, like vbsr_matrix_create, requires scalar offsets that start at
+ * 0), expands it to scalar CSR in the reference's order (rows, then blocks in
+ * row_ptr order, then columns) and copies that to the current HIP device;
+ * it rejects rhs outside {8,16,32,64} and matrices of 2^31 or more stored
+ * values (32-bit CSR indices).  vbsr_csr_plan_execute enqueues C = A * B with
+ * rocsparse_spmm (default algorithm); the first call also creates the dense
+ * descriptors and allocates the workspace, which later calls reuse.  Not
+ * thread-safe, like the reference's baseline plans (README.md:88). */
+typedef struct vbsr_csr_plan vbsr_csr_plan;
+int vbsr_csr_plan_create(const vbsr_host_view* host, int32_t rhs, vbsr_csr_plan** out);
+void vbsr_csr_plan_destroy(vbsr_csr_plan* plan);
+int vbsr_csr_plan_execute(vbsr_csr_plan* plan, const float* B, float* C, hipStream_t stream);
+/* ScalarCsrPlan::workspace_bytes (vbsr.hpp:131-132): bytes of workspace
+ * allocated by the first execute (0 before it, and for a null plan). */
+int64_t vbsr_csr_plan_workspace_bytes(const vbsr_csr_plan* plan);
+
 #ifdef __cplusplus
 }
 #endif

@@ -105,6 +105,8 @@ void run_negative_tests() {
   vbsr::Matrix device(valid);
   expect_invalid_argument([&] { vbsr::Plan plan(device, {7, vbsr::Kernel::RowOwned}); }, "invalid RHS accepted");
   expect_invalid_argument([&] { vbsr::Plan plan(device, {8, vbsr::Kernel::SplitRow}); }, "split-row accepted");
+  expect_invalid_argument([&] { vbsr::ScalarCsrPlan plan(valid, 12); }, "CSR plan accepted an invalid RHS");
+  expect_invalid_argument([&] { vbsr::ScalarCsrPlan plan(bad, 8); }, "CSR plan accepted an invalid host matrix");
   options.degree = 5;
   expect_invalid_argument([&] { vbsr::generate(options); }, "degree > block_cols accepted");
 }
@@ -158,6 +160,16 @@ void run_case(vbsr::Distribution distribution, int degree, int rhs, bool local, 
   if (std::memcmp(scalar.data(), emulated.data(), scalar.size() * sizeof(float)) != 0)
     throw std::runtime_error("row-owned scalar differs from the fmaf-order emulation" + tag);
 
+  // The library baseline, as test_main.cpp:96-97 runs the cuSPARSE plan.
+  vbsr::ScalarCsrPlan csr(host, rhs);
+  if (csr.workspace_bytes() != 0) throw std::runtime_error("workspace before the first execute" + tag);
+  for (int run = 0; run < 2; ++run) {
+    c.poison();
+    csr.execute(b.ptr, c.ptr, stream);
+    hip_ok(hipStreamSynchronize(stream), "sync");
+    compare(c.read(), reference, bound, "rocSPARSE CSR" + tag);
+  }
+
   hip_ok(hipStreamDestroy(stream), "hipStreamDestroy");
 }
 
@@ -186,8 +198,8 @@ int main() {
     run_negative_tests();
     const int cases = run_parameter_matrix();
     std::cout << "PASS: negative tests + " << cases
-              << " parameter cases (MFMA plan + order-preserving kernel, non-default stream, NaN-poisoned C, "
-                 "bit-identical repeats)\n";
+              << " parameter cases (MFMA plan + order-preserving kernel + rocSPARSE CSR plan, non-default "
+                 "stream, NaN-poisoned C, bit-identical repeats)\n";
     return 0;
   } catch (const std::exception& error) {
     std::cerr << "FAIL: " << error.what() << '\n';

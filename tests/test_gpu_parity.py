@@ -329,3 +329,64 @@ def test_cpp_api_program():
     note(result.stdout.strip() + result.stderr.strip())
     assert result.returncode == 0
     assert result.stdout.startswith("PASS")
+
+
+# ---- the rocSPARSE scalar-CSR baseline (reference ScalarCsrPlan) -----------
+
+def run_csr(c, plan, b_dev=None, c_dev=None):
+    b_dev = c.b_dev if b_dev is None else b_dev
+    c_dev = c.c_dev if c_dev is None else c_dev
+    c_dev.fill_(float("nan"))
+    torch.cuda.current_stream(DEVICE).synchronize()
+    with torch.cuda.stream(c.stream):
+        plan.execute(b_dev, c_dev, c.stream)
+    c.stream.synchronize()
+    return c_dev.cpu().numpy().copy()
+
+
+@pytest.mark.parametrize("case", reference_cases(), ids=lambda c: f"{c[0]}-d{c[1]}-n{c[2]}-{c[3]}-s{c[4]}")
+def test_scalar_csr_plan_reference_matrix(case):
+    """tests/test_main.cpp:84-97: the library baseline on every parameter case."""
+    distribution, degree, rhs, locality, seed = case
+    note(f"csr {case}")
+    host = vb.generate(9, 17, degree, distribution, locality, seed)
+    c = Case(host, rhs, seed)
+    try:
+        plan = vb.ScalarCsrPlan(host, rhs)
+        assert plan.workspace_bytes() == 0
+        c.check_tolerance(run_csr(c, plan), "rocSPARSE CSR")
+        c.check_tolerance(run_csr(c, plan), "rocSPARSE CSR (second run)")
+        plan.close()
+    finally:
+        c.close()
+
+
+@pytest.mark.parametrize("config", [("config2", 1024, 8, "low", "random", 16, 2),
+                                    ("config3", 4096, 8, "high", "random", 32, 1)], ids=lambda c: c[0])
+def test_scalar_csr_plan_baseline_configs(config):
+    name, rows, degree, distribution, locality, rhs, seed = config
+    note(f"csr {config}")
+    host = vb.generate(rows, rows, degree, distribution, locality, seed)
+    c = Case(host, rhs, seed)
+    try:
+        plan = vb.ScalarCsrPlan(host, rhs)
+        c.check_tolerance(run_csr(c, plan), f"rocSPARSE CSR {name}")
+        plan.close()
+    finally:
+        c.close()
+
+
+def test_scalar_csr_plan_follows_new_dense_pointers():
+    """The dense descriptors made at the first execute take the next call's B and C."""
+    host = vb.generate(40, 40, 4, "high", "random", 21)
+    c = Case(host, 16, 21)
+    try:
+        plan = vb.ScalarCsrPlan(host, 16)
+        c.check_tolerance(run_csr(c, plan), "first pointers")
+        b2 = (c.b_dev * 2.0).contiguous()
+        c2 = torch.empty_like(c.c_dev)
+        doubled = run_csr(c, plan, b2, c2)
+        np.testing.assert_allclose(doubled, 2.0 * c.reference, rtol=1e-5, atol=1e-4)
+        plan.close()
+    finally:
+        c.close()

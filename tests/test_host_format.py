@@ -134,3 +134,19 @@ def test_launchers_reject_bad_rhs_before_touching_the_gpu():
             vb.launch_row_owned(view, vb.RowSchedule(), None, None, rhs)
         with pytest.raises(ValueError):
             vb.launch_row_owned_scalar(view, None, None, rhs)
+
+
+def test_csr_plan_rejects_bad_input_before_touching_the_gpu():
+    host = vb.generate(4, 6, 2, "high", "random", 5)
+    for rhs in (0, 12, 128):
+        with pytest.raises(ValueError):
+            vb.ScalarCsrPlan(host, rhs)
+    bad = host.copy()
+    bad.row_size[0] = 7
+    with pytest.raises(ValueError):
+        vb.ScalarCsrPlan(bad, 8)
+    lib = vb.library()
+    assert lib.vbsr_csr_plan_create(None, 8, None) == vb.VBSR_INVALID_ARGUMENT
+    assert lib.vbsr_csr_plan_execute(None, None, None, None) == vb.VBSR_INVALID_ARGUMENT
+    assert lib.vbsr_csr_plan_workspace_bytes(None) == 0
+    lib.vbsr_csr_plan_destroy(None)

@@ -84,6 +84,10 @@ SIGNATURES = {
     "vbsr_launch_row_owned": (ctypes.c_int, [ctypes.POINTER(DeviceView), ctypes.POINTER(RowSchedule), _P, _P,
                                              ctypes.c_int32, _P]),
     "vbsr_launch_row_owned_scalar": (ctypes.c_int, [ctypes.POINTER(DeviceView), _P, _P, ctypes.c_int32, _P]),
+    "vbsr_csr_plan_create": (ctypes.c_int, [ctypes.POINTER(HostView), ctypes.c_int32, ctypes.POINTER(_P)]),
+    "vbsr_csr_plan_destroy": (None, [_P]),
+    "vbsr_csr_plan_execute": (ctypes.c_int, [_P, _P, _P, _P]),
+    "vbsr_csr_plan_workspace_bytes": (ctypes.c_int64, [_P]),
 }
 
 _lib = None
@@ -305,3 +309,37 @@ def launch_row_owned_scalar(device_view, B, C, rhs, stream=None):
     """launch_row_owned_scalar (vbsr.hpp:161): the reference-order kernel."""
     _check(library().vbsr_launch_row_owned_scalar(ctypes.byref(device_view), _address(B), _address(C), int(rhs),
                                                   _stream(stream)))
+
+
+class ScalarCsrPlan:
+    """The rocSPARSE scalar-CSR baseline (reference ScalarCsrPlan, vbsr.hpp:121-136): the host matrix is
+    expanded to CSR and copied to the device; execute runs rocsparse_spmm.  Not thread-safe."""
+
+    def __init__(self, host, rhs_width):
+        handle = ctypes.c_void_p()
+        view = host._view()
+        _check(library().vbsr_csr_plan_create(ctypes.byref(view), int(rhs_width), ctypes.byref(handle)))
+        self._handle = handle
+        self.rhs_width = int(rhs_width)
+        self.scalar_rows = host.scalar_rows
+        self.scalar_cols = host.scalar_cols
+
+    def close(self):
+        if getattr(self, "_handle", None):
+            library().vbsr_csr_plan_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def execute(self, B, C, stream=None):
+        """Enqueues C = A*B on `stream`; the first call also allocates the workspace."""
+        _check_panel(B, self.scalar_cols * self.rhs_width, "B")
+        _check_panel(C, self.scalar_rows * self.rhs_width, "C")
+        _check(library().vbsr_csr_plan_execute(self._handle, _address(B), _address(C), _stream(stream)))
+
+    def workspace_bytes(self):
+        return library().vbsr_csr_plan_workspace_bytes(self._handle)

@@ -9,7 +9,8 @@
 //                                (record, run, record, wait);
 //   useful_gflops                2 * rhs * sum(h * w) / gpu median
 //                                (benchmark.cpp:197-207);
-//   launches, workspace_bytes    kernels per run, bytes of workspace (0).
+//   launches, workspace_bytes    kernels per run, bytes of workspace (only the
+//                                rocSPARSE plan has one).
 //
 // Columns appended after the reference's: the same repetitions with a 1 GiB
 // read-only sweep before each one (inputs in HBM only), the algorithmic bytes
@@ -23,8 +24,10 @@
 // asks for the reference test's uniform [-1, 1] stream.
 //
 // Methods: row_owned_hybrid (Plan::execute with Kernel::RowOwned, the
-// reference's tuned path) and row_owned_scalar (launch_row_owned_scalar).
-// The reference's cuSPARSE and cuBLAS baselines have no counterpart here.
+// reference's tuned path), row_owned_scalar (launch_row_owned_scalar) and
+// scalar_csr_rocsparse (ScalarCsrPlan, the counterpart of the reference's
+// scalar_csr_cusparse row).  The reference's grouped cuBLAS baseline has no
+// counterpart here.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -257,21 +260,24 @@ int run(const Arguments& a) {
     std::cout << "method,block_rows,degree,distribution,locality,rhs,seed,"
                  "gpu_median_ms,gpu_p95_ms,hot_median_ms,hot_p95_ms,useful_gflops,"
                  "launches,workspace_bytes,cold_median_ms,cold_p95_ms,algorithmic_bytes,cold_gbs,identical\n";
-  auto report = [&](const char* method, const Timing& t, int launches) {
+  auto report = [&](const char* method, const Timing& t, int launches, size_t workspace) {
     std::cout << method << ',' << a.rows << ',' << a.degree << ',' << a.distribution << ',' << a.locality << ','
               << a.rhs_width << ',' << a.seed << ',' << std::fixed << std::setprecision(5) << t.gpu_median << ','
               << t.gpu_p95 << ',' << t.host_median << ',' << t.host_p95 << ','
-              << useful_flops / (t.gpu_median * 1e6) << ',' << launches << ',' << 0 << ',' << t.cold_median << ','
+              << useful_flops / (t.gpu_median * 1e6) << ',' << launches << ',' << workspace << ',' << t.cold_median << ','
               << t.cold_p95 << ',' << std::setprecision(0) << bytes << ',' << std::setprecision(2)
               << (t.cold_median > 0 ? bytes / (t.cold_median * 1e6) : 0.0) << ',' << (t.identical ? 1 : 0) << '\n'
               << std::flush;
   };
   report("row_owned_hybrid", bench.time([&](hipStream_t s) { plan.execute(b, c, s); }, a, c, c_count),
-         plan.launch_count());
+         plan.launch_count(), 0);
   report("row_owned_scalar",
          bench.time([&](hipStream_t s) { vbsr::launch_row_owned_scalar(view, b, c, a.rhs_width, s); }, a, c,
                     c_count),
-         1);
+         1, 0);
+  vbsr::ScalarCsrPlan csr(host, a.rhs_width);
+  const Timing csr_timing = bench.time([&](hipStream_t s) { csr.execute(b, c, s); }, a, c, c_count);
+  report("scalar_csr_rocsparse", csr_timing, 1, csr.workspace_bytes());
   hip_check(hipFree(b), "hipFree");
   hip_check(hipFree(c), "hipFree");
   return 0;

@@ -17,6 +17,10 @@ struct vbsr_matrix {
 struct vbsr_plan {
   vbsr_amd::Plan plan;
 };
+struct vbsr_csr_plan {
+  vbsr_amd::CsrPlan plan;
+  vbsr_csr_plan(const vbsr_host_view& host, int rhs) : plan(host, rhs) {}
+};
 
 namespace {
 
@@ -160,6 +164,28 @@ int vbsr_launch_row_owned_scalar(const vbsr_device_view* matrix, const float* B,
     require(matrix, "matrix");
     vbsr_amd::launch_scalar(*matrix, B, C, rhs, stream);
   });
+}
+
+int vbsr_csr_plan_create(const vbsr_host_view* host, int32_t rhs, vbsr_csr_plan** out) {
+  return guarded([&] {
+    require(host, "host");
+    require(out, "out");
+    *out = nullptr;
+    *out = new vbsr_csr_plan(*host, rhs);
+  });
+}
+
+void vbsr_csr_plan_destroy(vbsr_csr_plan* plan) { delete plan; }
+
+int vbsr_csr_plan_execute(vbsr_csr_plan* plan, const float* B, float* C, hipStream_t stream) {
+  return guarded([&] {
+    require(plan, "plan");
+    plan->plan.execute(B, C, stream);
+  });
+}
+
+int64_t vbsr_csr_plan_workspace_bytes(const vbsr_csr_plan* plan) {
+  return plan ? int64_t(plan->plan.workspace_bytes()) : 0;
 }
 
 }  // extern "C"

@@ -110,6 +110,55 @@ bool row_owned_supported(const vbsr_device_view& a, const float* b);
 void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& schedule, const float* b, float* c,
                       int rhs, hipStream_t stream);
 
+// ---- scalar CSR baseline on rocSPARSE (csr_baseline.cpp) ------------------
+
+// The VBSR matrix expanded to scalar CSR in the reference's order
+// (cusparse_baseline.cu:35-64): rows in order, blocks in row_ptr order, each
+// block's columns ascending.
+struct ScalarCsr {
+  std::vector<int32_t> row_offsets;  // scalar_rows + 1
+  std::vector<int32_t> columns;
+  std::vector<float> values;
+};
+ScalarCsr expand_to_scalar_csr(const vbsr_host_view& host);
+
+}  // namespace vbsr_amd
+
+// rocSPARSE's opaque handle types (rocsparse-types.h), declared here so that
+// only csr_baseline.cpp includes rocSPARSE.
+typedef struct _rocsparse_handle* rocsparse_handle;
+typedef struct _rocsparse_spmat_descr* rocsparse_spmat_descr;
+typedef struct _rocsparse_dnmat_descr* rocsparse_dnmat_descr;
+
+namespace vbsr_amd {
+
+// ScalarCsrPlan (reference vbsr.hpp:121-136): device CSR copy plus a
+// rocSPARSE SpMM whose dense descriptors and workspace are created at the
+// first execute.  Not thread-safe, like the reference's.
+class CsrPlan {
+public:
+  CsrPlan(const vbsr_host_view& host, int rhs);
+  ~CsrPlan();
+  CsrPlan(const CsrPlan&) = delete;
+  CsrPlan& operator=(const CsrPlan&) = delete;
+  void execute(const float* b, float* c, hipStream_t stream);
+  size_t workspace_bytes() const { return workspace_bytes_; }
+
+private:
+  int rhs_{};
+  int64_t rows_{}, cols_{}, nnz_{};
+  int32_t* row_offsets_{};
+  int32_t* columns_{};
+  float* values_{};
+  void* workspace_{};
+  size_t workspace_bytes_{};
+  rocsparse_handle handle_{};
+  rocsparse_spmat_descr matrix_{};
+  rocsparse_dnmat_descr input_{};
+  rocsparse_dnmat_descr output_{};
+  void release() noexcept;
+};
+
 // ---- plan (plan.cpp) -------------------------------------------------------
 
 struct Plan {
