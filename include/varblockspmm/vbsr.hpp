@@ -6,9 +6,9 @@
 // Differences from the reference header:
 //  - cpu_reference is not part of the library.  It is the test oracle and
 //    lives in oracle/vbsr_oracle.h (orc_cpu_reference).
-//  - ScalarCsrPlan runs on rocSPARSE instead of cuSPARSE.  GroupedGemmPlan
-//    (the cuBLAS grouped-GEMM baseline) and the one-shot baseline helpers
-//    are not provided.
+//  - ScalarCsrPlan runs on rocSPARSE instead of cuSPARSE, and GroupedGemmPlan
+//    on rocBLAS (one batched GEMM per slot and block shape) instead of
+//    cuBLAS grouped GEMM.  The one-shot baseline helpers are not provided.
 //  - Distribution gains Bimodal8or64 and Tied8to64; GeneratorOptions gains
 //    clamp_local_columns (clamped instead of cyclic local columns).
 //  - launch_row_owned takes the matrix's row schedule instead of the
@@ -214,6 +214,34 @@ private:
     void operator()(vbsr_csr_plan* p) const { vbsr_csr_plan_destroy(p); }
   };
   std::unique_ptr<vbsr_csr_plan, Destroy> plan_;
+};
+
+/** Persistent rocBLAS baseline that groups equally shaped blocks of each
+ * block slot into batched GEMMs (reference GroupedGemmPlan, vbsr.hpp:138-152).
+ * Not thread-safe. */
+class GroupedGemmPlan {
+public:
+  GroupedGemmPlan(const HostMatrix& matrix, int rhs_width) {
+    const vbsr_host_view v = matrix.view();
+    vbsr_gemm_plan* handle = nullptr;
+    detail::check(vbsr_gemm_plan_create(&v, rhs_width, &handle));
+    plan_.reset(handle);
+  }
+  GroupedGemmPlan(const GroupedGemmPlan&) = delete;
+  GroupedGemmPlan& operator=(const GroupedGemmPlan&) = delete;
+  /** Enqueues all grouped GEMM batches on `stream`. */
+  void execute(const float* B, float* C, hipStream_t stream = 0) {
+    detail::check(vbsr_gemm_plan_execute(plan_.get(), B, C, stream));
+  }
+  /** Returns the number of sequential block slots. */
+  int launch_count() const { return vbsr_gemm_plan_launch_count(plan_.get()); }
+  size_t workspace_bytes() const { return 0; }
+
+private:
+  struct Destroy {
+    void operator()(vbsr_gemm_plan* p) const { vbsr_gemm_plan_destroy(p); }
+  };
+  std::unique_ptr<vbsr_gemm_plan, Destroy> plan_;
 };
 
 /** The tuned row-owned kernels (reference vbsr.hpp:158-159). */

@@ -187,6 +187,22 @@ int vbsr_csr_plan_execute(vbsr_csr_plan* plan, const float* B, float* C, hipStre
  * allocated by the first execute (0 before it, and for a null plan). */
 int64_t vbsr_csr_plan_workspace_bytes(const vbsr_csr_plan* plan);
 
+/* GroupedGemmPlan (vbsr.hpp:138-152; slot_split.cu:22-145): the slot-grouped
+ * library baseline, on rocBLAS.  Slot s holds the s-th block of every block
+ * row; within a slot, blocks are grouped by (h, w).  vbsr_gemm_plan_create
+ * validates the host matrix (scalar offsets must start at 0), rejects rhs
+ * outside {8,16,32,64} and copies the packed values to the current HIP
+ * device.  vbsr_gemm_plan_execute zeroes C and runs the slots in order, one
+ * rocblas_sgemm_batched call per (slot, shape) group (rocBLAS has no grouped
+ * batched GEMM).  Not thread-safe, like the reference's baseline plans. */
+typedef struct vbsr_gemm_plan vbsr_gemm_plan;
+int vbsr_gemm_plan_create(const vbsr_host_view* host, int32_t rhs, vbsr_gemm_plan** out);
+void vbsr_gemm_plan_destroy(vbsr_gemm_plan* plan);
+int vbsr_gemm_plan_execute(vbsr_gemm_plan* plan, const float* B, float* C, hipStream_t stream);
+/* GroupedGemmPlan::launch_count (vbsr.hpp:146-147): the number of block
+ * slots, i.e. the largest block-row degree (0 for a null plan). */
+int vbsr_gemm_plan_launch_count(const vbsr_gemm_plan* plan);
+
 #ifdef __cplusplus
 }
 #endif

@@ -107,6 +107,8 @@ void run_negative_tests() {
   expect_invalid_argument([&] { vbsr::Plan plan(device, {8, vbsr::Kernel::SplitRow}); }, "split-row accepted");
   expect_invalid_argument([&] { vbsr::ScalarCsrPlan plan(valid, 12); }, "CSR plan accepted an invalid RHS");
   expect_invalid_argument([&] { vbsr::ScalarCsrPlan plan(bad, 8); }, "CSR plan accepted an invalid host matrix");
+  expect_invalid_argument([&] { vbsr::GroupedGemmPlan plan(valid, 24); }, "grouped plan accepted an invalid RHS");
+  expect_invalid_argument([&] { vbsr::GroupedGemmPlan plan(bad, 8); }, "grouped plan accepted an invalid matrix");
   options.degree = 5;
   expect_invalid_argument([&] { vbsr::generate(options); }, "degree > block_cols accepted");
 }
@@ -169,6 +171,12 @@ void run_case(vbsr::Distribution distribution, int degree, int rhs, bool local, 
     hip_ok(hipStreamSynchronize(stream), "sync");
     compare(c.read(), reference, bound, "rocSPARSE CSR" + tag);
   }
+  vbsr::GroupedGemmPlan grouped(host, rhs);
+  if (grouped.launch_count() != degree) throw std::runtime_error("grouped launch_count != degree" + tag);
+  c.poison();
+  grouped.execute(b.ptr, c.ptr, stream);
+  hip_ok(hipStreamSynchronize(stream), "sync");
+  compare(c.read(), reference, bound, "grouped rocBLAS" + tag);
 
   hip_ok(hipStreamDestroy(stream), "hipStreamDestroy");
 }
@@ -198,8 +206,8 @@ int main() {
     run_negative_tests();
     const int cases = run_parameter_matrix();
     std::cout << "PASS: negative tests + " << cases
-              << " parameter cases (MFMA plan + order-preserving kernel + rocSPARSE CSR plan, non-default "
-                 "stream, NaN-poisoned C, bit-identical repeats)\n";
+              << " parameter cases (MFMA plan + order-preserving kernel + rocSPARSE CSR plan + grouped "
+                 "rocBLAS plan, non-default stream, NaN-poisoned C, bit-identical repeats)\n";
     return 0;
   } catch (const std::exception& error) {
     std::cerr << "FAIL: " << error.what() << '\n';

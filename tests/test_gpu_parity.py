@@ -390,3 +390,41 @@ def test_scalar_csr_plan_follows_new_dense_pointers():
         plan.close()
     finally:
         c.close()
+
+
+# ---- the rocBLAS slot-grouped baseline (reference GroupedGemmPlan) ---------
+
+@pytest.mark.parametrize("case", reference_cases(), ids=lambda c: f"{c[0]}-d{c[1]}-n{c[2]}-{c[3]}-s{c[4]}")
+def test_grouped_gemm_plan_reference_matrix(case):
+    """tests/test_main.cpp:86-99: the grouped-GEMM baseline on every parameter case."""
+    distribution, degree, rhs, locality, seed = case
+    note(f"grouped {case}")
+    host = vb.generate(9, 17, degree, distribution, locality, seed)
+    c = Case(host, rhs, seed)
+    try:
+        plan = vb.GroupedGemmPlan(host, rhs)
+        assert plan.launch_count() == degree
+        c.check_tolerance(run_csr(c, plan), "grouped rocBLAS")
+        plan.close()
+    finally:
+        c.close()
+
+
+def test_grouped_gemm_plan_config3_and_empty_rows():
+    note("grouped config3 + empty rows")
+    host = vb.generate(4096, 4096, 8, "high", "random", 1)
+    c = Case(host, 32, 1)
+    try:
+        plan = vb.GroupedGemmPlan(host, 32)
+        c.check_tolerance(run_csr(c, plan), "grouped rocBLAS config3")
+        plan.close()
+    finally:
+        c.close()
+    empty = hand_made([8, 16, 24, 32], [8, 64, 40], [[], [0, 2], [], [1]])
+    c = Case(empty, 16, 3)
+    try:
+        plan = vb.GroupedGemmPlan(empty, 16)
+        c.check_tolerance(run_csr(c, plan), "grouped rocBLAS empty rows")  # empty rows must come out 0
+        plan.close()
+    finally:
+        c.close()

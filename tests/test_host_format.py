@@ -150,3 +150,19 @@ def test_csr_plan_rejects_bad_input_before_touching_the_gpu():
     assert lib.vbsr_csr_plan_execute(None, None, None, None) == vb.VBSR_INVALID_ARGUMENT
     assert lib.vbsr_csr_plan_workspace_bytes(None) == 0
     lib.vbsr_csr_plan_destroy(None)
+
+
+def test_grouped_gemm_plan_rejects_bad_input_before_touching_the_gpu():
+    host = vb.generate(4, 6, 2, "high", "random", 5)
+    for rhs in (0, 24, 128):
+        with pytest.raises(ValueError):
+            vb.GroupedGemmPlan(host, rhs)
+    bad = host.copy()
+    bad.row_size[0] = 7
+    with pytest.raises(ValueError):
+        vb.GroupedGemmPlan(bad, 8)
+    lib = vb.library()
+    assert lib.vbsr_gemm_plan_create(None, 8, None) == vb.VBSR_INVALID_ARGUMENT
+    assert lib.vbsr_gemm_plan_execute(None, None, None, None) == vb.VBSR_INVALID_ARGUMENT
+    assert lib.vbsr_gemm_plan_launch_count(None) == 0
+    lib.vbsr_gemm_plan_destroy(None)

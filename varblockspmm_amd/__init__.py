@@ -88,6 +88,10 @@ SIGNATURES = {
     "vbsr_csr_plan_destroy": (None, [_P]),
     "vbsr_csr_plan_execute": (ctypes.c_int, [_P, _P, _P, _P]),
     "vbsr_csr_plan_workspace_bytes": (ctypes.c_int64, [_P]),
+    "vbsr_gemm_plan_create": (ctypes.c_int, [ctypes.POINTER(HostView), ctypes.c_int32, ctypes.POINTER(_P)]),
+    "vbsr_gemm_plan_destroy": (None, [_P]),
+    "vbsr_gemm_plan_execute": (ctypes.c_int, [_P, _P, _P, _P]),
+    "vbsr_gemm_plan_launch_count": (ctypes.c_int, [_P]),
 }
 
 _lib = None
@@ -343,3 +347,41 @@ class ScalarCsrPlan:
 
     def workspace_bytes(self):
         return library().vbsr_csr_plan_workspace_bytes(self._handle)
+
+
+class GroupedGemmPlan:
+    """The rocBLAS slot-grouped baseline (reference GroupedGemmPlan, vbsr.hpp:138-152): slot s holds the
+    s-th block of every block row, grouped by block shape; one batched GEMM per (slot, shape).
+    Not thread-safe."""
+
+    def __init__(self, host, rhs_width):
+        handle = ctypes.c_void_p()
+        view = host._view()
+        _check(library().vbsr_gemm_plan_create(ctypes.byref(view), int(rhs_width), ctypes.byref(handle)))
+        self._handle = handle
+        self.rhs_width = int(rhs_width)
+        self.scalar_rows = host.scalar_rows
+        self.scalar_cols = host.scalar_cols
+
+    def close(self):
+        if getattr(self, "_handle", None):
+            library().vbsr_gemm_plan_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def execute(self, B, C, stream=None):
+        """Enqueues C = A*B on `stream` (C is zeroed first)."""
+        _check_panel(B, self.scalar_cols * self.rhs_width, "B")
+        _check_panel(C, self.scalar_rows * self.rhs_width, "C")
+        _check(library().vbsr_gemm_plan_execute(self._handle, _address(B), _address(C), _stream(stream)))
+
+    def launch_count(self):
+        return library().vbsr_gemm_plan_launch_count(self._handle)
+
+    def workspace_bytes(self):
+        return 0

@@ -26,8 +26,8 @@
 // Methods: row_owned_hybrid (Plan::execute with Kernel::RowOwned, the
 // reference's tuned path), row_owned_scalar (launch_row_owned_scalar) and
 // scalar_csr_rocsparse (ScalarCsrPlan, the counterpart of the reference's
-// scalar_csr_cusparse row).  The reference's grouped cuBLAS baseline has no
-// counterpart here.
+// scalar_csr_cusparse row) and slot_grouped_rocblas (GroupedGemmPlan, the
+// counterpart of slot_grouped_cublas).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -278,6 +278,9 @@ int run(const Arguments& a) {
   vbsr::ScalarCsrPlan csr(host, a.rhs_width);
   const Timing csr_timing = bench.time([&](hipStream_t s) { csr.execute(b, c, s); }, a, c, c_count);
   report("scalar_csr_rocsparse", csr_timing, 1, csr.workspace_bytes());
+  vbsr::GroupedGemmPlan grouped(host, a.rhs_width);
+  report("slot_grouped_rocblas", bench.time([&](hipStream_t s) { grouped.execute(b, c, s); }, a, c, c_count),
+         grouped.launch_count(), 0);
   hip_check(hipFree(b), "hipFree");
   hip_check(hipFree(c), "hipFree");
   return 0;

@@ -21,6 +21,10 @@ struct vbsr_csr_plan {
   vbsr_amd::CsrPlan plan;
   vbsr_csr_plan(const vbsr_host_view& host, int rhs) : plan(host, rhs) {}
 };
+struct vbsr_gemm_plan {
+  vbsr_amd::GemmPlan plan;
+  vbsr_gemm_plan(const vbsr_host_view& host, int rhs) : plan(host, rhs) {}
+};
 
 namespace {
 
@@ -187,5 +191,25 @@ int vbsr_csr_plan_execute(vbsr_csr_plan* plan, const float* B, float* C, hipStre
 int64_t vbsr_csr_plan_workspace_bytes(const vbsr_csr_plan* plan) {
   return plan ? int64_t(plan->plan.workspace_bytes()) : 0;
 }
+
+int vbsr_gemm_plan_create(const vbsr_host_view* host, int32_t rhs, vbsr_gemm_plan** out) {
+  return guarded([&] {
+    require(host, "host");
+    require(out, "out");
+    *out = nullptr;
+    *out = new vbsr_gemm_plan(*host, rhs);
+  });
+}
+
+void vbsr_gemm_plan_destroy(vbsr_gemm_plan* plan) { delete plan; }
+
+int vbsr_gemm_plan_execute(vbsr_gemm_plan* plan, const float* B, float* C, hipStream_t stream) {
+  return guarded([&] {
+    require(plan, "plan");
+    plan->plan.execute(B, C, stream);
+  });
+}
+
+int vbsr_gemm_plan_launch_count(const vbsr_gemm_plan* plan) { return plan ? plan->plan.launch_count() : 0; }
 
 }  // extern "C"

@@ -159,6 +159,52 @@ private:
   void release() noexcept;
 };
 
+// ---- slot-grouped GEMM baseline on rocBLAS (gemm_baseline.cpp) -------------
+
+}  // namespace vbsr_amd
+
+// rocBLAS's opaque handle type (rocblas-types.h), declared here so that only
+// gemm_baseline.cpp includes rocBLAS.
+typedef struct _rocblas_handle* rocblas_handle;
+
+namespace vbsr_amd {
+
+// Writes b_pointers[i] = b + b_offset[i] and c_pointers[i] = c + c_offset[i]
+// for i < count on `stream` (batch_pointers.hip).
+void fill_batch_pointers(const int64_t* b_offset, const int64_t* c_offset, int64_t count, const float* b, float* c,
+                         const float** b_pointers, float** c_pointers, hipStream_t stream);
+
+// GroupedGemmPlan (reference vbsr.hpp:138-152): one rocblas_sgemm_batched
+// call per (slot, block shape).  Not thread-safe, like the reference's.
+class GemmPlan {
+public:
+  GemmPlan(const vbsr_host_view& host, int rhs);
+  ~GemmPlan();
+  GemmPlan(const GemmPlan&) = delete;
+  GemmPlan& operator=(const GemmPlan&) = delete;
+  void execute(const float* b, float* c, hipStream_t stream);
+  // Sequential block slots (the reference's launch_count, slot_split.cu:137).
+  int launch_count() const { return int(slots_.size()); }
+
+private:
+  struct Group {
+    int32_t h, w;   // block shape
+    int64_t first;  // first entry of the pointer arrays
+    int32_t count;  // blocks of this shape in the slot
+  };
+  int rhs_{};
+  int64_t rows_{}, cols_{}, entries_{};
+  std::vector<std::vector<Group>> slots_;
+  float* values_{};
+  const float** a_pointers_{};
+  int64_t* b_offset_{};
+  int64_t* c_offset_{};
+  const float** b_pointers_{};
+  float** c_pointers_{};
+  rocblas_handle handle_{};
+  void release() noexcept;
+};
+
 // ---- plan (plan.cpp) -------------------------------------------------------
 
 struct Plan {
