@@ -68,9 +68,10 @@ struct HostSchedule {
   int64_t groups{};            // workgroups of one launch (multiple of kXcds)
 };
 
-// Step records plus the launch order of the block rows: each XCD gets a
-// contiguous band of block rows (its B slices stay in that XCD's L2 when
-// columns are local), heaviest rows first within a band.  Deterministic.
+// Step records plus the launch order of the block rows: each row goes to the
+// XCD whose eighth of the block columns holds most of its block widths (so
+// an XCD's B slices concentrate in one eighth of B), with equal work per XCD;
+// heaviest rows first within an XCD.  Deterministic.
 HostSchedule build_schedule(const vbsr_host_view& host);
 
 // ---- device format (device_matrix.cpp) ----------------------------------

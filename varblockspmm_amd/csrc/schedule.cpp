@@ -9,13 +9,19 @@
 //    the kernel never walks block metadata: a wave loads the records of all
 //    its steps of a row with one load;
 //  * one workgroup owns one block row;
-//  * workgroups are dispatched to the 8 XCDs round-robin by index, so the
-//    block rows are cut into 8 contiguous bands and band x is placed at
-//    indices x, x + 8, x + 16, ...: each XCD works through one band, and the
-//    B slices of a band stay in that XCD's L2 when columns are local;
+//  * workgroups are dispatched to the 8 XCDs round-robin by index, so each
+//    XCD's rows (its band) are placed at indices x, x + 8, x + 16, ...;
+//  * a block row goes to the XCD whose eighth of the block columns holds the
+//    largest share of the row's block widths, as long as that XCD holds less
+//    than an eighth of the total work (else to its next best eighth): the B
+//    slices an XCD reads then concentrate in one eighth of B, which its L2
+//    keeps; rows with the most concentrated columns are placed first, and
+//    equal work per XCD keeps any XCD from finishing late.  With local
+//    columns this gives contiguous bands of rows;
 //  * within a band, heavier rows are dispatched first, so the light ones fill
 //    the tail of the launch.
 #include <algorithm>
+#include <array>
 #include <numeric>
 
 #include "internal.hpp"
@@ -48,23 +54,57 @@ HostSchedule build_schedule(const vbsr_host_view& m) {
   for (int32_t i = 0; i < rows; ++i)
     work[size_t(i)] = int64_t((m.row_size[i] + 15) / 16) * (step_first[size_t(i) + 1] - step_first[size_t(i)]) + 8;
 
-  const int64_t per_xcd = (int64_t(rows) + kXcds - 1) / kXcds;
+  // Home eighth of each row: the eighth of the block columns holding the
+  // largest share of its block widths.
+  const int32_t cols = m.block_cols;
+  std::vector<std::array<int64_t, kXcds>> share(static_cast<size_t>(rows));
+  for (int32_t i = 0; i < rows; ++i) {
+    share[size_t(i)].fill(0);
+    for (int32_t blk = m.row_ptr[i]; blk < m.row_ptr[i + 1]; ++blk) {
+      const int32_t c = m.block_col[blk];
+      share[size_t(i)][size_t(std::min<int64_t>(kXcds - 1, int64_t(c) * kXcds / cols))] += m.col_size[c];
+    }
+  }
+  auto top_share = [&](int32_t i) { return *std::max_element(share[size_t(i)].begin(), share[size_t(i)].end()); };
+  std::vector<int32_t> order(static_cast<size_t>(rows));
+  std::iota(order.begin(), order.end(), 0);
+  std::stable_sort(order.begin(), order.end(), [&](int32_t x, int32_t y) { return top_share(x) > top_share(y); });
+
+  const int64_t total = std::accumulate(work.begin(), work.end(), int64_t(0));
+  const int64_t cap = total / kXcds + 1;
+  std::array<int64_t, kXcds> load{};
+  std::vector<std::vector<int32_t>> bands(kXcds);
+  for (const int32_t i : order) {
+    std::array<int, kXcds> rank{};
+    std::iota(rank.begin(), rank.end(), 0);
+    std::stable_sort(rank.begin(), rank.end(),
+                     [&](int x, int y) { return share[size_t(i)][size_t(x)] > share[size_t(i)][size_t(y)]; });
+    int chosen = -1;
+    for (const int x : rank)
+      if (load[size_t(x)] + work[size_t(i)] <= cap) {
+        chosen = x;
+        break;
+      }
+    if (chosen < 0) chosen = int(std::min_element(load.begin(), load.end()) - load.begin());
+    bands[size_t(chosen)].push_back(i);
+    load[size_t(chosen)] += work[size_t(i)];
+  }
+
+  int64_t per_xcd = 0;
+  for (auto& band : bands) {
+    std::stable_sort(band.begin(), band.end(), [&](int32_t x, int32_t y) { return work[size_t(x)] > work[size_t(y)]; });
+    per_xcd = std::max<int64_t>(per_xcd, int64_t(band.size()));
+  }
   out.groups = per_xcd * kXcds;
   RowItem padding{};
   padding.step_count = -1;
   padding.row = -1;
   out.rows.assign(size_t(out.groups), padding);
-  std::vector<int32_t> band;
   for (int xcd = 0; xcd < kXcds; ++xcd) {
-    const int64_t lo = std::min<int64_t>(rows, xcd * per_xcd);
-    const int64_t hi = std::min<int64_t>(rows, lo + per_xcd);
-    band.resize(size_t(hi - lo));
-    std::iota(band.begin(), band.end(), int32_t(lo));
-    std::stable_sort(band.begin(), band.end(),
-                     [&](int32_t x, int32_t y) { return work[size_t(x)] > work[size_t(y)]; });
-    for (int64_t pos = 0; pos < hi - lo; ++pos) {
-      const int32_t i = band[size_t(pos)];
-      RowItem& item = out.rows[size_t(pos * kXcds + xcd)];
+    const auto& band = bands[size_t(xcd)];
+    for (size_t pos = 0; pos < band.size(); ++pos) {
+      const int32_t i = band[pos];
+      RowItem& item = out.rows[pos * kXcds + size_t(xcd)];
       item.c_off = m.row_scalar_off[i];
       item.step_first = step_first[size_t(i)];
       item.step_count = step_first[size_t(i) + 1] - step_first[size_t(i)];
