@@ -136,7 +136,21 @@ def cpu_baseline(host, b, rhs, budget_s=20.0):
         oracle_ffi.cpu_reference(oracle_host, b, rhs)
         times.append(time.perf_counter() - t0)
     times.sort()
-    return reference, oracle_host, {"median_s": times[len(times) // 2], "reps": reps, "warmup": 1}
+    return reference, oracle_host, {"median_s": times[len(times) // 2], "p95_s": percentile_95(times), "reps": reps,
+                                    "warmup": 1}
+
+
+def cpu_config1():
+    """The CPU-only benchmark configuration 1 (1024 block rows, degree 4, high block sizes, clamped
+    local columns, RHS 8, seed 1): the same oracle timing, single thread."""
+    import varblockspmm_amd as vb
+
+    host = vb.generate(1024, 1024, 4, "high", "clamped", 1)
+    b = vb.make_random_input(host.scalar_cols * 8, 1)
+    _, _, timing = cpu_baseline(host, b, 8)
+    return {"median_ms": round(timing["median_s"] * 1e3, 3), "p95_ms": round(timing["p95_s"] * 1e3, 3),
+            "reps": timing["reps"], "warmup": 1, "sum_hw": int(host.values.size),
+            "workload": "config 1: 1024 block rows, degree 4, high block sizes, clamped local columns, rhs 8, seed 1"}
 
 
 def main():
@@ -255,7 +269,8 @@ def main():
                    "sample": f"full workload: oracle cpu_reference (vbsr.cpp:167-201 restated in C) on the same "
                              f"instance and B, {cpu_timing['warmup']} warmup + {cpu_timing['reps']} reps, "
                              f"single thread; host {platform.processor() or platform.machine()}, "
-                             f"nproc {os.cpu_count()}"}
+                             f"nproc {os.cpu_count()}",
+                   "config1": cpu_config1()}
 
     traffic = None
     traffic_file = os.path.join(ROOT, "profiles", f"traffic_r{args.rows}_d{args.degree}_{args.distribution}_"
