@@ -428,3 +428,88 @@ def test_grouped_gemm_plan_config3_and_empty_rows():
         plan.close()
     finally:
         c.close()
+
+
+# ---- the largest B offsets ------------------------------------------------
+
+def largest_offset_case(scalar_cols, rhs):
+    """Three block rows over scalar_cols / 64 block columns of width 64, using the first, a middle
+    and the last block column, and a B panel (ld = scalar_cols) that is zero except where those
+    columns are read.  The panel is scalar_cols * rhs floats (2-4 GiB); np.zeros leaves its
+    untouched pages unallocated on the host."""
+    ncols = scalar_cols // 64
+    host = hand_made([16, 40, 8], [64] * ncols, [[0, ncols - 1], [ncols // 2], [ncols - 1]], seed=5)
+    rng = np.random.default_rng(9)
+    b = np.zeros(scalar_cols * rhs, dtype=np.float32)
+    for col in sorted({0, ncols // 2, ncols - 1}):
+        for n in range(rhs):
+            start = n * scalar_cols + col * 64
+            b[start:start + 64] = rng.uniform(-1, 1, 64).astype(np.float32)
+    return host, b
+
+
+def check_against_oracle(host, b, rhs, result, name):
+    oracle = as_oracle(host)
+    reference = o.cpu_reference(oracle, b, rhs)
+    bound = o.abs_product_sum(oracle, b, rhs)
+    assert np.all(np.isfinite(result)), name
+    max_abs, rel_l2, normwise, elementwise = o.parity_errors(result, reference, bound)
+    note(f"  {name}: max_abs={max_abs:.3g} rel_l2={rel_l2:.3g} normwise={normwise:.3g} elementwise={elementwise:.3g}")
+    assert max_abs <= 5e-4 and rel_l2 <= 5e-5, name
+    assert normwise <= NORMWISE_TOL and rel_l2 <= REL_L2_TOL and elementwise <= ELEMENTWISE_TOL, name
+
+
+def test_largest_b_offsets_take_the_mfma_kernel():
+    """K = 2^26 - 64, the largest K the MFMA kernel takes: its 32-bit B offsets reach
+    15 * K * 4 + 64 bytes, just under 2^32."""
+    scalar_cols, rhs = (1 << 26) - 64, 16
+    note(f"largest offsets: K={scalar_cols} rhs={rhs} (B {scalar_cols * rhs * 4 / 2**30:.1f} GiB)")
+    host, b = largest_offset_case(scalar_cols, rhs)
+    matrix = vb.Matrix(host)
+    try:
+        stream = torch.cuda.Stream(device=DEVICE)
+        b_dev = torch.from_numpy(b).to(DEVICE)
+        c_dev = torch.full((host.scalar_rows * rhs,), float("nan"), device=DEVICE)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            vb.launch_row_owned(matrix.device_view(), matrix.row_schedule(), b_dev, c_dev, rhs, stream)
+        stream.synchronize()
+        check_against_oracle(host, b, rhs, c_dev.cpu().numpy(), "launch_row_owned")
+        c_dev.fill_(float("nan"))
+        torch.cuda.synchronize()
+        plan = vb.Plan(matrix, rhs)
+        with torch.cuda.stream(stream):
+            plan.execute(b_dev, c_dev, stream)
+        stream.synchronize()
+        check_against_oracle(host, b, rhs, c_dev.cpu().numpy(), "plan")
+        plan.close()
+        del b_dev, c_dev
+    finally:
+        matrix.close()
+
+
+def test_k_at_the_offset_limit_goes_to_the_order_preserving_kernel():
+    """K = 2^26: the MFMA launcher refuses it and the plan runs the order-preserving kernel."""
+    scalar_cols, rhs = 1 << 26, 8
+    note(f"offset limit: K={scalar_cols} rhs={rhs}")
+    host, b = largest_offset_case(scalar_cols, rhs)
+    matrix = vb.Matrix(host)
+    try:
+        stream = torch.cuda.Stream(device=DEVICE)
+        b_dev = torch.from_numpy(b).to(DEVICE)
+        c_dev = torch.full((host.scalar_rows * rhs,), float("nan"), device=DEVICE)
+        torch.cuda.synchronize()
+        with pytest.raises(ValueError):
+            vb.launch_row_owned(matrix.device_view(), matrix.row_schedule(), b_dev, c_dev, rhs, stream)
+        plan = vb.Plan(matrix, rhs)
+        with torch.cuda.stream(stream):
+            plan.execute(b_dev, c_dev, stream)
+        stream.synchronize()
+        result = c_dev.cpu().numpy()
+        check_against_oracle(host, b, rhs, result, "plan at the limit")
+        expected = o.fmaf_order(as_oracle(host), b, rhs)
+        assert result.tobytes() == expected.tobytes(), "plan did not take the order-preserving kernel"
+        plan.close()
+        del b_dev, c_dev
+    finally:
+        matrix.close()
