@@ -513,3 +513,63 @@ def test_k_at_the_offset_limit_goes_to_the_order_preserving_kernel():
         del b_dev, c_dev
     finally:
         matrix.close()
+
+
+# ---- execute is stateless: concurrent streams, graph capture ---------------
+
+def test_concurrent_executes_on_two_streams():
+    """Plan::execute keeps no state (no workspace, no atomics): two plans of one matrix run
+    concurrently on two streams with their own B and C, and each matches its serial result."""
+    host = vb.generate(512, 512, 8, "high", "random", 31)
+    matrix = vb.Matrix(host)
+    try:
+        outs = []
+        runs = []
+        for rhs, seed in ((32, 1), (16, 2)):
+            b = torch.from_numpy(o.make_random_input(host.scalar_cols * rhs, seed)).to(DEVICE)
+            c = torch.full((host.scalar_rows * rhs,), float("nan"), device=DEVICE)
+            runs.append((vb.Plan(matrix, rhs), b, c, torch.cuda.Stream(device=DEVICE)))
+        serial = []
+        for plan, b, c, stream in runs:
+            with torch.cuda.stream(stream):
+                plan.execute(b, c, stream)
+            stream.synchronize()
+            serial.append(c.cpu().numpy().copy())
+            c.fill_(float("nan"))
+        torch.cuda.synchronize()
+        for _ in range(20):  # interleave many launches on both streams
+            for plan, b, c, stream in runs:
+                with torch.cuda.stream(stream):
+                    plan.execute(b, c, stream)
+        torch.cuda.synchronize()
+        for (plan, b, c, stream), expected in zip(runs, serial):
+            assert c.cpu().numpy().tobytes() == expected.tobytes()
+            plan.close()
+    finally:
+        matrix.close()
+
+
+def test_plan_execute_replays_from_a_hip_graph():
+    """execute enqueues one kernel and allocates nothing, so it can be captured into a HIP graph;
+    every replay, with eager work and synchronisations between replays, equals the eager result."""
+    host = vb.generate(256, 256, 8, "high", "random", 41)
+    c = Case(host, 32, 41)
+    try:
+        plan = vb.Plan(c.matrix, 32)
+        eager = c.run_plan(plan)
+        c.check_tolerance(eager, "eager")
+        capture_stream = torch.cuda.Stream(device=DEVICE)
+        graph = torch.cuda.CUDAGraph()
+        c.c_dev.fill_(float("nan"))
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=capture_stream):
+            plan.execute(c.b_dev, c.c_dev, capture_stream)
+        for replay in range(5):
+            c.c_dev.fill_(float("nan"))       # eager work between replays
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert c.c_dev.cpu().numpy().tobytes() == eager.tobytes(), f"replay {replay}"
+        plan.close()
+    finally:
+        c.close()
