@@ -140,6 +140,37 @@ def cpu_baseline(host, b, rhs, budget_s=20.0):
                                     "warmup": 1}
 
 
+def cpu_threads():
+    """Host threads this process may use: OMP_NUM_THREADS when set, else its CPU affinity."""
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = os.cpu_count() or 1
+    requested = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return max(1, min(allowed, requested) if requested > 0 else allowed)
+
+
+def cpu_parallel(oracle_host, b, rhs, reference, budget_s=10.0):
+    """A multi-core CPU baseline owned by this build (the reference is single-threaded): the oracle's
+    cpu_reference with block rows spread over OpenMP threads, bit-identical to the serial result."""
+    import numpy as np
+    import oracle_ffi
+
+    threads = cpu_threads()
+    t0 = time.perf_counter()
+    result = oracle_ffi.cpu_reference_threads(oracle_host, b, rhs, threads)  # warmup
+    first = time.perf_counter() - t0
+    reps = max(3, min(20, int(budget_s / max(first, 1e-3)) - 1))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        oracle_ffi.cpu_reference_threads(oracle_host, b, rhs, threads)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return threads, bool(np.array_equal(result, reference)), {"median_s": times[len(times) // 2],
+                                                              "p95_s": percentile_95(times), "reps": reps}
+
+
 def cpu_config1():
     """The CPU-only benchmark configuration 1 (1024 block rows, degree 4, high block sizes, clamped
     local columns, RHS 8, seed 1): the same oracle timing, single thread."""
@@ -271,6 +302,14 @@ def main():
                              f"single thread; host {platform.processor() or platform.machine()}, "
                              f"nproc {os.cpu_count()}",
                    "config1": cpu_config1()}
+            threads, identical, par = cpu_parallel(oracle_host, b_host, args.rhs, reference)
+            cpu["parallel"] = {
+                "value": work["bytes"] / par["median_s"] / 1e9, "unit": "GB/s", "cores": threads,
+                "kind": "build-owned", "median_ms": par["median_s"] * 1e3, "p95_ms": par["p95_s"] * 1e3,
+                "bit_identical_to_serial": identical,
+                "sample": f"full workload: the same oracle cpu_reference with block rows spread over {threads} "
+                          f"OpenMP threads (not in the reference, which is single-threaded), 1 warmup + "
+                          f"{par['reps']} reps"}
 
     traffic = None
     traffic_file = os.path.join(ROOT, "profiles", f"traffic_r{args.rows}_d{args.degree}_{args.distribution}_"

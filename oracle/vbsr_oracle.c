@@ -21,6 +21,9 @@
  *   orc_cpu_reference         brute force on dense expansions, closed forms
  *                             (identity blocks, unit-vector B, linearity,
  *                             degree-1 batched GEMM).
+ *   orc_cpu_reference_threads bit-identical to orc_cpu_reference (each
+ *                             row's arithmetic is unchanged; rows run in
+ *                             parallel).
  *   orc_fmaf_order            same checks as orc_cpu_reference within fp32
  *                             tolerance; bit-exact emulation pins the GPU
  *                             order-preserving kernel.
@@ -326,26 +329,42 @@ static int64_t scalar_rows(const orc_view* a) { return a->row_scalar_off[a->bloc
 static int64_t scalar_cols(const orc_view* a) { return a->col_scalar_off[a->block_cols]; }
 
 /* src/format/vbsr.cpp:167-201 */
+/* One block row of cpu_reference (vbsr.cpp:176-199): C's rows of block row i
+ * are written by this call only. */
+static void reference_row(const orc_view* a, const float* b, int32_t rhs, int64_t M, int64_t K, int32_t i,
+                          float* c) {
+  const int32_t h = a->row_size[i];
+  for (int32_t blk = a->row_ptr[i]; blk < a->row_ptr[i + 1]; ++blk) {
+    const int32_t col = a->block_col[blk];
+    const int32_t w = a->col_size[col];
+    const float* A = a->values + a->value_off[blk];
+    for (int32_t r = 0; r < h; ++r) {
+      for (int32_t n = 0; n < rhs; ++n) {
+        const float* Bn = b + a->col_scalar_off[col] + (int64_t)n * K;
+        double sum = 0.0;
+        for (int32_t k = 0; k < w; ++k) sum += (double)A[r + (int64_t)k * h] * (double)Bn[k];
+        c[a->row_scalar_off[i] + r + (int64_t)n * M] += (float)sum;
+      }
+    }
+  }
+}
+
 int orc_cpu_reference(const orc_view* a, const float* b, int64_t b_len, int32_t rhs, float* c) {
   const int64_t M = scalar_rows(a), K = scalar_cols(a);
   if (b_len != K * rhs) return ORC_INVALID; /* :169-171 */
   memset(c, 0, sizeof(float) * (size_t)(M * rhs)); /* :175 */
-  for (int32_t i = 0; i < a->block_rows; ++i) {
-    const int32_t h = a->row_size[i];
-    for (int32_t blk = a->row_ptr[i]; blk < a->row_ptr[i + 1]; ++blk) {
-      const int32_t col = a->block_col[blk];
-      const int32_t w = a->col_size[col];
-      const float* A = a->values + a->value_off[blk];
-      for (int32_t r = 0; r < h; ++r) {
-        for (int32_t n = 0; n < rhs; ++n) {
-          const float* Bn = b + a->col_scalar_off[col] + (int64_t)n * K;
-          double sum = 0.0;
-          for (int32_t k = 0; k < w; ++k) sum += (double)A[r + (int64_t)k * h] * (double)Bn[k];
-          c[a->row_scalar_off[i] + r + (int64_t)n * M] += (float)sum;
-        }
-      }
-    }
-  }
+  for (int32_t i = 0; i < a->block_rows; ++i) reference_row(a, b, rhs, M, K, i, c);
+  return ORC_OK;
+}
+
+int orc_cpu_reference_threads(const orc_view* a, const float* b, int64_t b_len, int32_t rhs, int32_t threads,
+                              float* c) {
+  const int64_t M = scalar_rows(a), K = scalar_cols(a);
+  if (b_len != K * rhs || threads < 1) return ORC_INVALID;
+  memset(c, 0, sizeof(float) * (size_t)(M * rhs));
+  const int32_t rows = a->block_rows;
+#pragma omp parallel for schedule(dynamic, 16) num_threads(threads)
+  for (int32_t i = 0; i < rows; ++i) reference_row(a, b, rhs, M, K, i, c);
   return ORC_OK;
 }
 

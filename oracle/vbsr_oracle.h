@@ -129,6 +129,14 @@ int orc_validate(const orc_view* view, int* rule);
  * Returns ORC_INVALID when B's length differs from scalar_cols * rhs. */
 int orc_cpu_reference(const orc_view* a, const float* b, int64_t b_len, int32_t rhs, float* c);
 
+/* orc_cpu_reference with its block rows spread over `threads` OpenMP
+ * threads.  Each row's arithmetic and order are unchanged and no two rows
+ * write the same output, so C is bit-identical to orc_cpu_reference's.  Not
+ * in the reference, which is single-threaded: a multi-core CPU baseline.
+ * Returns ORC_INVALID for a wrong B length or threads < 1. */
+int orc_cpu_reference_threads(const orc_view* a, const float* b, int64_t b_len, int32_t rhs, int32_t threads,
+                              float* c);
+
 /* Per-output sum over all contributing products of |a|*|b|, in double: the
  * scale of the elementwise error bound. */
 int orc_abs_product_sum(const orc_view* a, const float* b, int64_t b_len, int32_t rhs,

@@ -79,6 +79,9 @@ def lib():
                                ("orc_abs_product_sum", ctypes.c_double)):
             getattr(L, name).argtypes = [ctypes.POINTER(OrcView), ctypes.POINTER(ctypes.c_float), ctypes.c_int64,
                                          ctypes.c_int32, ctypes.POINTER(out_type)]
+        L.orc_cpu_reference_threads.argtypes = [ctypes.POINTER(OrcView), ctypes.POINTER(ctypes.c_float),
+                                                ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
+                                                ctypes.POINTER(ctypes.c_float)]
         L.orc_make_random_input.argtypes = [ctypes.c_int64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_float)]
         L.orc_useful_flops.restype = ctypes.c_double
         L.orc_useful_flops.argtypes = [ctypes.POINTER(OrcView), ctypes.c_int32]
@@ -196,6 +199,18 @@ def _product(name, matrix, b, rhs, dtype):
 def cpu_reference(matrix, b, rhs):
     """C = A*B, column-major M x rhs, double per-block dots (vbsr.cpp:167-201)."""
     return _product("orc_cpu_reference", matrix, b, rhs, np.float32)
+
+
+def cpu_reference_threads(matrix, b, rhs, threads):
+    """cpu_reference with block rows spread over `threads` OpenMP threads; bit-identical to it."""
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    out = np.empty(matrix.scalar_rows * rhs, dtype=np.float32)
+    view = matrix.view()
+    status = lib().orc_cpu_reference_threads(ctypes.byref(view), b.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                             len(b), rhs, threads, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+    if status != 0:
+        raise ValueError("B size or thread count")
+    return out
 
 
 def fmaf_order(matrix, b, rhs):

@@ -321,6 +321,22 @@ def test_cpu_reference_empty_and_duplicate_blocks():
     np.testing.assert_allclose(o.fmaf_order(m, b, rhs).reshape(rhs, -1), want, rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("threads", [1, 3, 8])
+def test_threaded_cpu_reference_is_bit_identical(threads):
+    """The multi-core baseline keeps each row's arithmetic, so its bits equal the serial oracle's."""
+    for args, rhs in (((300, 300, 8, "high", "random", 5), 32), ((9, 17, 4, "bimodal", "local", 6), 8)):
+        m = o.generate(*args)
+        b = o.make_random_input(m.scalar_cols * rhs, args[-1])
+        np.testing.assert_array_equal(o.cpu_reference_threads(m, b, rhs, threads), o.cpu_reference(m, b, rhs))
+    m = _rows_with_empty()
+    b = o.make_random_input(m.scalar_cols * 8, 3)
+    np.testing.assert_array_equal(o.cpu_reference_threads(m, b, 8, threads), o.cpu_reference(m, b, 8))
+    with pytest.raises(ValueError):
+        o.cpu_reference_threads(m, b[:-1], 8, threads)
+    with pytest.raises(ValueError):
+        o.cpu_reference_threads(m, b, 8, 0)
+
+
 def test_identity_blocks_copy_b():
     """Degree 1, block column i for row i, A_i = I: C equals B exactly."""
     sizes = np.array([8, 24, 64, 16])
