@@ -134,10 +134,11 @@ int64_t vbsr_matrix_scalar_cols(const vbsr_matrix* matrix);
  * counts (vbsr.cpp:96-102), which Plan passes to launch_row_owned.  Device
  * arrays owned by the matrix; opaque to callers. */
 typedef struct vbsr_row_schedule {
-  const void* steps;  /* device: one 16-byte record per k step */
-  const void* rows;   /* device: one 32-byte row item per workgroup */
-  int64_t groups;     /* workgroups of one launch */
-  int32_t step_limit; /* index of the last step record */
+  const void* steps;     /* device: one 16-byte record per k step */
+  const void* rows;      /* device: one 32-byte row item per workgroup, launch order for rhs 8 and 16 */
+  int64_t groups;        /* workgroups of one launch */
+  int32_t step_limit;    /* index of the last step record */
+  const void* rows_wide; /* device: the same row items, launch order for rhs 32 and 64 */
 } vbsr_row_schedule;
 int vbsr_matrix_row_schedule(const vbsr_matrix* matrix, vbsr_row_schedule* out);
 

@@ -1,0 +1,193 @@
+// CPU checks of the row schedule (varblockspmm_amd/csrc/schedule.cpp), built
+// from the library's own sources without a GPU.  For each matrix:
+//   * the step records cover every block of every row exactly once, in
+//     row_ptr order, with the A and B offsets the kernel reads;
+//   * both launch orders hold every block row once, padding slots have
+//     step_count < 0, and each row item describes its row;
+//   * both orders place each row on the same XCD (workgroup index mod 8), and
+//     no XCD's work exceeds an eighth of the total by more than one row's;
+//   * `rows` runs each XCD's rows heaviest first; `rows_wide` ends each XCD's
+//     band with its lightest quarter, heaviest first;
+//   * building twice gives the same schedule.
+// Prints one line per matrix and exits non-zero if any check fails.
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include "internal.hpp"
+
+namespace {
+
+int failures = 0;
+
+#define CHECK(cond)                                                              \
+  do {                                                                           \
+    if (!(cond)) {                                                               \
+      std::fprintf(stderr, "FAILED %s:%d: %s\n", __FILE__, __LINE__, #cond);     \
+      ++failures;                                                                \
+      return;                                                                    \
+    }                                                                            \
+  } while (0)
+
+int64_t row_work(const vbsr_amd::RowItem& item) {
+  return int64_t((item.h + 15) / 16) * item.step_count + 8;
+}
+
+void check_order(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s, const std::vector<vbsr_amd::RowItem>& items,
+                 std::vector<int>& xcd_of_row, bool wide) {
+  using vbsr_amd::kXcds;
+  CHECK(int64_t(items.size()) == s.groups);
+  CHECK(s.groups % kXcds == 0);
+  std::vector<int> seen(size_t(m.block_rows), 0);
+  std::vector<int64_t> load(kXcds, 0);
+  std::vector<std::vector<int64_t>> band_work(kXcds);
+  bool padding_started[kXcds] = {};
+  for (int64_t g = 0; g < s.groups; ++g) {
+    const auto& item = items[size_t(g)];
+    const int xcd = int(g % kXcds);
+    if (item.step_count < 0) {
+      padding_started[xcd] = true;
+      continue;
+    }
+    CHECK(!padding_started[xcd]);  // padding only after an XCD's last row
+    const int32_t i = item.row;
+    CHECK(i >= 0 && i < m.block_rows);
+    CHECK(++seen[size_t(i)] == 1);
+    CHECK(item.c_off == m.row_scalar_off[i]);
+    CHECK(item.h == m.row_size[i]);
+    if (xcd_of_row[size_t(i)] < 0) xcd_of_row[size_t(i)] = xcd;
+    CHECK(xcd_of_row[size_t(i)] == xcd);
+    load[size_t(xcd)] += row_work(item);
+    band_work[size_t(xcd)].push_back(row_work(item));
+  }
+  for (int32_t i = 0; i < m.block_rows; ++i) CHECK(seen[size_t(i)] == 1);
+  int64_t heaviest = 0;
+  for (const auto& band : band_work)
+    for (const int64_t w : band) heaviest = std::max(heaviest, w);
+  // Placement fills an XCD up to an eighth of the work (+1) and only then
+  // falls back to the least loaded one.
+  int64_t total = 0;
+  for (const int64_t l : load) total += l;
+  CHECK(*std::max_element(load.begin(), load.end()) <= total / kXcds + 1 + heaviest);
+  for (const auto& band : band_work) {
+    const size_t tail = wide ? band.size() / 4 : band.size();
+    const size_t from = band.size() - tail;
+    for (size_t q = from + 1; q < band.size(); ++q) CHECK(band[q - 1] >= band[q]);
+    if (wide && tail > 0) {
+      const int64_t tail_max = *std::max_element(band.begin() + std::ptrdiff_t(from), band.end());
+      for (size_t q = 0; q < from; ++q) CHECK(band[q] >= tail_max);
+    }
+  }
+}
+
+void check_steps(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s) {
+  const auto& items = s.rows;
+  std::vector<const vbsr_amd::RowItem*> by_row(size_t(m.block_rows), nullptr);
+  for (const auto& item : items)
+    if (item.step_count >= 0) by_row[size_t(item.row)] = &item;
+  int64_t expected_first = 0;
+  for (int32_t i = 0; i < m.block_rows; ++i) {
+    const auto* item = by_row[size_t(i)];
+    CHECK(item != nullptr);
+    CHECK(item->step_first == expected_first);
+    int32_t step = item->step_first;
+    const int32_t h = m.row_size[i];
+    for (int32_t blk = m.row_ptr[i]; blk < m.row_ptr[i + 1]; ++blk) {
+      const int32_t col = m.block_col[blk];
+      const int32_t w = m.col_size[col];
+      int32_t k0 = 0;
+      while (k0 < w) {
+        CHECK(step < item->step_first + item->step_count);
+        const auto& rec = s.steps[size_t(step)];
+        const bool half = (rec.b_off & vbsr_amd::kHalfStep) != 0;
+        CHECK(half == (w - k0 == 8));
+        CHECK(rec.a_off == m.value_off[blk] + int64_t(k0) * h);
+        CHECK((rec.b_off & (vbsr_amd::kHalfStep - 1)) == m.col_scalar_off[col] + k0);
+        k0 += half ? 8 : 16;
+        ++step;
+      }
+      CHECK(k0 == w);
+    }
+    CHECK(step == item->step_first + item->step_count);
+    expected_first = step;
+  }
+  CHECK(int64_t(s.steps.size()) == expected_first);
+}
+
+bool same(const std::vector<vbsr_amd::RowItem>& a, const std::vector<vbsr_amd::RowItem>& b) {
+  return a.size() == b.size() && (a.empty() || std::memcmp(a.data(), b.data(), a.size() * sizeof(a[0])) == 0);
+}
+
+void check_host(const vbsr_amd::HostMatrix& host, const char* name) {
+  const vbsr_host_view m = host.view();
+  vbsr_amd::validate(m);
+  const vbsr_amd::HostSchedule s = vbsr_amd::build_schedule(m);
+  const int before = failures;
+  check_steps(m, s);
+  std::vector<int> xcd_of_row(size_t(m.block_rows), -1);
+  check_order(m, s, s.rows, xcd_of_row, false);
+  check_order(m, s, s.rows_wide, xcd_of_row, true);
+  const vbsr_amd::HostSchedule again = vbsr_amd::build_schedule(m);
+  if (!(same(s.rows, again.rows) && same(s.rows_wide, again.rows_wide) && s.steps.size() == again.steps.size())) {
+    std::fprintf(stderr, "FAILED: schedule not deterministic\n");
+    ++failures;
+  }
+  std::printf("%s %s groups=%lld steps=%zu\n", failures == before ? "ok" : "FAILED", name,
+              static_cast<long long>(s.groups), s.steps.size());
+}
+
+// Three block rows, the middle one empty; block widths 8 (one half step),
+// 24 (a full and a half step) and 64 (four full steps).
+vbsr_amd::HostMatrix with_empty_row() {
+  vbsr_amd::HostMatrix h;
+  h.block_rows = 3;
+  h.block_cols = 3;
+  h.row_ptr = {0, 2, 2, 4};
+  h.block_col = {0, 2, 1, 2};
+  h.row_size = {16, 8, 40};
+  h.col_size = {8, 24, 64};
+  h.row_scalar_off = {0, 16, 24, 64};
+  h.col_scalar_off = {0, 8, 32, 96};
+  h.value_off = {0, 16 * 8, 16 * 8 + 16 * 64, 16 * 8 + 16 * 64 + 40 * 24, 16 * 8 + 16 * 64 + 40 * 24 + 40 * 64};
+  h.values.assign(size_t(h.value_off.back()), 1.0f);
+  return h;
+}
+
+}  // namespace
+
+int main() {
+  const int32_t shapes[][5] = {
+      // rows, cols, degree, distribution, locality
+      {4096, 4096, 8, VBSR_DIST_HIGH_VARIANCE, VBSR_LOCALITY_RANDOM},
+      {4096, 4096, 8, VBSR_DIST_HIGH_VARIANCE, VBSR_LOCALITY_LOCAL},
+      {1024, 1024, 4, VBSR_DIST_HIGH_VARIANCE, VBSR_LOCALITY_LOCAL_CLAMPED},
+      {1024, 1024, 8, VBSR_DIST_LOW_VARIANCE, VBSR_LOCALITY_RANDOM},
+      {4096, 4096, 16, VBSR_DIST_BIMODAL, VBSR_LOCALITY_RANDOM},
+      {4096, 4096, 1, VBSR_DIST_UNIFORM, VBSR_LOCALITY_RANDOM},
+      {9, 17, 4, VBSR_DIST_HIGH_VARIANCE, VBSR_LOCALITY_LOCAL},
+      {5, 3, 2, VBSR_DIST_BIMODAL, VBSR_LOCALITY_RANDOM},
+      {1, 1, 1, VBSR_DIST_UNIFORM, VBSR_LOCALITY_RANDOM},
+      {37, 64, 16, VBSR_DIST_LOW_VARIANCE, VBSR_LOCALITY_RANDOM},
+  };
+  uint64_t seed = 1;
+  for (const auto& shape : shapes) {
+    vbsr_generator_options options{};
+    options.block_rows = shape[0];
+    options.block_cols = shape[1];
+    options.degree = shape[2];
+    options.rhs_width = 32;
+    options.distribution = shape[3];
+    options.locality = shape[4];
+    options.seed = seed++;
+    char name[128];
+    std::snprintf(name, sizeof(name), "rows=%d degree=%d dist=%d locality=%d seed=%llu", options.block_rows,
+                  options.degree, options.distribution, options.locality,
+                  static_cast<unsigned long long>(options.seed));
+    check_host(vbsr_amd::generate(options), name);
+  }
+  check_host(with_empty_row(), "hand-made, empty middle row");
+  std::printf("%s\n", failures == 0 ? "ALL OK" : "FAILURES");
+  return failures == 0 ? 0 : 1;
+}

@@ -56,6 +56,7 @@ DeviceMatrix::DeviceMatrix(const vbsr_host_view& host) {
     view_.values = upload(host.values, host.values_len, allocations_);
     schedule_.steps = upload(schedule.steps.data(), int64_t(schedule.steps.size()), allocations_);
     schedule_.rows = upload(schedule.rows.data(), int64_t(schedule.rows.size()), allocations_);
+    schedule_.rows_wide = upload(schedule.rows_wide.data(), int64_t(schedule.rows_wide.size()), allocations_);
     schedule_.groups = schedule.groups;
     schedule_.step_limit = int32_t(std::max<size_t>(schedule.steps.size(), 1) - 1);
   } catch (...) {

@@ -63,15 +63,18 @@ struct alignas(16) RowItem {
 static_assert(sizeof(RowItem) == 32, "RowItem is read as 8 dwords");
 
 struct HostSchedule {
-  std::vector<StepRec> steps;  // row after row, blocks in row_ptr order
-  std::vector<RowItem> rows;   // one per workgroup, in launch order
-  int64_t groups{};            // workgroups of one launch (multiple of kXcds)
+  std::vector<StepRec> steps;      // row after row, blocks in row_ptr order
+  std::vector<RowItem> rows;       // one per workgroup, launch order for RHS 8 and 16
+  std::vector<RowItem> rows_wide;  // the same items, launch order for RHS 32 and 64
+  int64_t groups{};                // workgroups of one launch (multiple of kXcds)
 };
 
-// Step records plus the launch order of the block rows: each row goes to the
-// XCD whose eighth of the block columns holds most of its block widths (so
-// an XCD's B slices concentrate in one eighth of B), with equal work per XCD;
-// heaviest rows first within an XCD.  Deterministic.
+// Step records plus two launch orders of the block rows.  Both place each row
+// on the XCD whose eighth of the block columns holds most of its block widths
+// (so an XCD's B slices concentrate in one eighth of B), with equal work per
+// XCD.  Within an XCD, `rows` runs the heaviest rows first; `rows_wide` chains
+// rows that share block columns and keeps the lightest quarter last.
+// Deterministic.
 HostSchedule build_schedule(const vbsr_host_view& host);
 
 // ---- device format (device_matrix.cpp) ----------------------------------

@@ -345,7 +345,8 @@ void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& s, con
     throw std::invalid_argument("row-owned kernel needs a 16-byte aligned B and fewer than 2^26 scalar columns");
   if (s.groups <= 0) return;
   if (s.groups > int64_t(0x7fffffff)) throw std::invalid_argument("schedule too large for one launch");
-  const Launch L{a, static_cast<const StepRec*>(s.steps), static_cast<const RowItem*>(s.rows), s.step_limit, b, c};
+  const void* rows = rhs >= 32 && s.rows_wide != nullptr ? s.rows_wide : s.rows;
+  const Launch L{a, static_cast<const StepRec*>(s.steps), static_cast<const RowItem*>(rows), s.step_limit, b, c};
   switch (rhs) {
   case 8: launch<8>(L, s.groups, stream); break;
   case 16: launch<16>(L, s.groups, stream); break;

@@ -18,11 +18,20 @@
 //    keeps; rows with the most concentrated columns are placed first, and
 //    equal work per XCD keeps any XCD from finishing late.  With local
 //    columns this gives contiguous bands of rows;
-//  * within a band, heavier rows are dispatched first, so the light ones fill
-//    the tail of the launch.
+//  * within a band, two launch orders are kept.  For RHS 8 and 16 heavier
+//    rows are dispatched first, so the light ones fill the tail of the launch.
+//    For RHS 32 and 64, where B is most of the traffic, the heavier three
+//    quarters of the band are chained so that each row follows the rows it
+//    shares block columns (or neighbouring block columns, which share B's
+//    128-byte lines) with, and the lightest quarter follows, heaviest first.
+//    Chaining cuts the XCD's B line misses; keeping a light tail bounds the
+//    imbalance it costs.  On RHS 8 and 16, where A dominates, the imbalance
+//    outweighs the saving.
 #include <algorithm>
 #include <array>
 #include <numeric>
+#include <queue>
+#include <tuple>
 
 #include "internal.hpp"
 
@@ -96,22 +105,72 @@ HostSchedule build_schedule(const vbsr_host_view& m) {
     per_xcd = std::max<int64_t>(per_xcd, int64_t(band.size()));
   }
   out.groups = per_xcd * kXcds;
-  RowItem padding{};
-  padding.step_count = -1;
-  padding.row = -1;
-  out.rows.assign(size_t(out.groups), padding);
+
+  // Lays the bands out in launch order: the row at position pos of XCD x's
+  // band is workgroup pos * 8 + x; missing positions are padding slots.
+  auto emit = [&](const std::vector<std::vector<int32_t>>& ordered, std::vector<RowItem>& items) {
+    RowItem padding{};
+    padding.step_count = -1;
+    padding.row = -1;
+    items.assign(size_t(out.groups), padding);
+    for (int xcd = 0; xcd < kXcds; ++xcd) {
+      const auto& band = ordered[size_t(xcd)];
+      for (size_t pos = 0; pos < band.size(); ++pos) {
+        const int32_t i = band[pos];
+        RowItem& item = items[pos * kXcds + size_t(xcd)];
+        item.c_off = m.row_scalar_off[i];
+        item.step_first = step_first[size_t(i)];
+        item.step_count = step_first[size_t(i) + 1] - step_first[size_t(i)];
+        item.h = m.row_size[i];
+        item.row = i;
+      }
+    }
+  };
+  emit(bands, out.rows);
+
+  // Chained order of each band for RHS 32 and 64.  A row's affinity to the
+  // rows already placed counts 2 per shared block column and 1 per
+  // neighbouring one; the next row is the unplaced one of highest affinity,
+  // ties to the heavier (then earlier) row.  Affinities only grow, so a
+  // max-heap with stale entries skipped finds it.
+  std::vector<std::vector<int32_t>> users(static_cast<size_t>(cols));
+  std::vector<std::vector<int32_t>> chained(kXcds);
   for (int xcd = 0; xcd < kXcds; ++xcd) {
     const auto& band = bands[size_t(xcd)];
-    for (size_t pos = 0; pos < band.size(); ++pos) {
-      const int32_t i = band[pos];
-      RowItem& item = out.rows[pos * kXcds + size_t(xcd)];
-      item.c_off = m.row_scalar_off[i];
-      item.step_first = step_first[size_t(i)];
-      item.step_count = step_first[size_t(i) + 1] - step_first[size_t(i)];
-      item.h = m.row_size[i];
-      item.row = i;
+    const size_t n = band.size();
+    const size_t head = n - n / 4;  // rows chained; the rest is the light tail
+    for (auto& u : users) u.clear();
+    for (size_t q = 0; q < head; ++q)
+      for (int32_t blk = m.row_ptr[band[q]]; blk < m.row_ptr[band[q] + 1]; ++blk)
+        users[size_t(m.block_col[blk])].push_back(int32_t(q));
+    std::vector<int64_t> affinity(head, 0);
+    std::vector<char> placed(head, 0);
+    using Entry = std::tuple<int64_t, int64_t, int32_t>;  // affinity, work, -position
+    std::priority_queue<Entry> heap;
+    for (size_t q = 0; q < head; ++q) heap.emplace(0, work[size_t(band[q])], -int32_t(q));
+    auto& order_out = chained[size_t(xcd)];
+    while (!heap.empty()) {
+      const auto [a, w, neg] = heap.top();
+      heap.pop();
+      const size_t q = size_t(-neg);
+      if (placed[q] || a != affinity[q]) continue;
+      placed[q] = 1;
+      order_out.push_back(band[q]);
+      for (int32_t blk = m.row_ptr[band[q]]; blk < m.row_ptr[band[q] + 1]; ++blk) {
+        const int32_t c = m.block_col[blk];
+        for (int32_t d = -1; d <= 1; ++d) {
+          if (c + d < 0 || c + d >= cols) continue;
+          for (const int32_t r : users[size_t(c + d)]) {
+            if (placed[size_t(r)]) continue;
+            affinity[size_t(r)] += d == 0 ? 2 : 1;
+            heap.emplace(affinity[size_t(r)], work[size_t(band[size_t(r)])], -r);
+          }
+        }
+      }
     }
+    order_out.insert(order_out.end(), band.begin() + std::ptrdiff_t(head), band.end());
   }
+  emit(chained, out.rows_wide);
   return out;
 }
 
