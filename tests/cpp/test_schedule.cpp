@@ -8,9 +8,13 @@
 //     no XCD's work exceeds an eighth of the total by more than one row's;
 //   * `rows` runs each XCD's rows heaviest first; `rows_wide` ends each XCD's
 //     band with its lightest quarter, heaviest first;
-//   * building twice gives the same schedule.
+//   * building twice gives the same schedule;
+//   * matrices whose rows share few block columns (every row on the same 8
+//     columns; rows overlapping in 15 of 16 columns) build in seconds: the
+//     chained order's work does not grow with the square of a column's users.
 // Prints one line per matrix and exits non-zero if any check fails.
 #include <algorithm>
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -120,11 +124,15 @@ bool same(const std::vector<vbsr_amd::RowItem>& a, const std::vector<vbsr_amd::R
   return a.size() == b.size() && (a.empty() || std::memcmp(a.data(), b.data(), a.size() * sizeof(a[0])) == 0);
 }
 
-void check_host(const vbsr_amd::HostMatrix& host, const char* name) {
-  const vbsr_host_view m = host.view();
-  vbsr_amd::validate(m);
-  const vbsr_amd::HostSchedule s = vbsr_amd::build_schedule(m);
+void check_view(const vbsr_host_view& m, const char* name, double max_seconds) {
   const int before = failures;
+  const auto t0 = std::chrono::steady_clock::now();
+  const vbsr_amd::HostSchedule s = vbsr_amd::build_schedule(m);
+  const double seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+  if (seconds > max_seconds) {
+    std::fprintf(stderr, "FAILED: %s took %.2f s to schedule (limit %.0f s)\n", name, seconds, max_seconds);
+    ++failures;
+  }
   check_steps(m, s);
   std::vector<int> xcd_of_row(size_t(m.block_rows), -1);
   check_order(m, s, s.rows, xcd_of_row, false);
@@ -134,8 +142,37 @@ void check_host(const vbsr_amd::HostMatrix& host, const char* name) {
     std::fprintf(stderr, "FAILED: schedule not deterministic\n");
     ++failures;
   }
-  std::printf("%s %s groups=%lld steps=%zu\n", failures == before ? "ok" : "FAILED", name,
-              static_cast<long long>(s.groups), s.steps.size());
+  std::printf("%s %s groups=%lld steps=%zu schedule=%.3f s\n", failures == before ? "ok" : "FAILED", name,
+              static_cast<long long>(s.groups), s.steps.size(), seconds);
+}
+
+void check_host(const vbsr_amd::HostMatrix& host, const char* name) {
+  const vbsr_host_view m = host.view();
+  vbsr_amd::validate(m);
+  check_view(m, name, 30.0);
+}
+
+// Block row i uses block columns (i + j) mod cols, j < degree, all blocks
+// 64 x 64.  Only the metadata is built: the schedule never reads values.
+void check_shared_columns(int32_t rows, int32_t cols, int32_t degree) {
+  vbsr_amd::HostMatrix h;
+  h.block_rows = rows;
+  h.block_cols = cols;
+  h.row_ptr.push_back(0);
+  for (int32_t i = 0; i < rows; ++i) {
+    for (int32_t j = 0; j < degree; ++j) h.block_col.push_back((i + j) % cols);
+    h.row_ptr.push_back(int32_t(h.block_col.size()));
+  }
+  h.row_size.assign(size_t(rows), 64);
+  h.col_size.assign(size_t(cols), 64);
+  for (int32_t i = 0; i <= rows; ++i) h.row_scalar_off.push_back(int64_t(i) * 64);
+  for (int32_t c = 0; c <= cols; ++c) h.col_scalar_off.push_back(int64_t(c) * 64);
+  for (size_t b = 0; b <= h.block_col.size(); ++b) h.value_off.push_back(int64_t(b) * 64 * 64);
+  vbsr_host_view m = h.view();
+  m.values_len = h.value_off.back();
+  char name[96];
+  std::snprintf(name, sizeof(name), "shared columns: rows=%d cols=%d degree=%d", rows, cols, degree);
+  check_view(m, name, 10.0);
 }
 
 // Three block rows, the middle one empty; block widths 8 (one half step),
@@ -188,6 +225,8 @@ int main() {
     check_host(vbsr_amd::generate(options), name);
   }
   check_host(with_empty_row(), "hand-made, empty middle row");
+  check_shared_columns(16384, 8, 8);
+  check_shared_columns(65536, 16384, 16);
   std::printf("%s\n", failures == 0 ? "ALL OK" : "FAILURES");
   return failures == 0 ? 0 : 1;
 }

@@ -31,7 +31,6 @@
 #include <array>
 #include <numeric>
 #include <queue>
-#include <tuple>
 
 #include "internal.hpp"
 
@@ -132,7 +131,12 @@ HostSchedule build_schedule(const vbsr_host_view& m) {
   // rows already placed counts 2 per shared block column and 1 per
   // neighbouring one; the next row is the unplaced one of highest affinity,
   // ties to the heavier (then earlier) row.  Affinities only grow, so a
-  // max-heap with stale entries skipped finds it.
+  // max-heap with stale entries skipped finds it.  A block column used by
+  // more than kMaxUsers rows of the band adds no affinity: it says little
+  // about which rows belong together, and skipping it bounds the work by
+  // 3 * kMaxUsers updates per block instead of growing with the square of
+  // the rows that share a column.
+  constexpr size_t kMaxUsers = 64;
   std::vector<std::vector<int32_t>> users(static_cast<size_t>(cols));
   std::vector<std::vector<int32_t>> chained(kXcds);
   for (int xcd = 0; xcd < kXcds; ++xcd) {
@@ -143,29 +147,40 @@ HostSchedule build_schedule(const vbsr_host_view& m) {
     for (size_t q = 0; q < head; ++q)
       for (int32_t blk = m.row_ptr[band[q]]; blk < m.row_ptr[band[q] + 1]; ++blk)
         users[size_t(m.block_col[blk])].push_back(int32_t(q));
-    std::vector<int64_t> affinity(head, 0);
+    // Heap keys: affinity in the high word, then the lower position (the
+    // band is sorted heaviest first, so that is the heavier row).
+    auto key = [](uint64_t affinity, size_t q) { return (affinity << 32) | (0xffffffffu - uint32_t(q)); };
+    std::vector<uint32_t> affinity(head, 0), gain(head, 0);
     std::vector<char> placed(head, 0);
-    using Entry = std::tuple<int64_t, int64_t, int32_t>;  // affinity, work, -position
-    std::priority_queue<Entry> heap;
-    for (size_t q = 0; q < head; ++q) heap.emplace(0, work[size_t(band[q])], -int32_t(q));
+    std::vector<int32_t> touched;
+    std::priority_queue<uint64_t> heap;
+    for (size_t q = 0; q < head; ++q) heap.push(key(0, q));
     auto& order_out = chained[size_t(xcd)];
     while (!heap.empty()) {
-      const auto [a, w, neg] = heap.top();
+      const uint64_t top = heap.top();
       heap.pop();
-      const size_t q = size_t(-neg);
-      if (placed[q] || a != affinity[q]) continue;
+      const size_t q = 0xffffffffu - uint32_t(top);
+      if (placed[q] || (top >> 32) != affinity[q]) continue;  // placed, or a stale entry
       placed[q] = 1;
       order_out.push_back(band[q]);
+      // Gains of the rows this placement touches, summed first so that each
+      // touched row is pushed once.
+      touched.clear();
       for (int32_t blk = m.row_ptr[band[q]]; blk < m.row_ptr[band[q] + 1]; ++blk) {
         const int32_t c = m.block_col[blk];
         for (int32_t d = -1; d <= 1; ++d) {
-          if (c + d < 0 || c + d >= cols) continue;
+          if (c + d < 0 || c + d >= cols || users[size_t(c + d)].size() > kMaxUsers) continue;
           for (const int32_t r : users[size_t(c + d)]) {
             if (placed[size_t(r)]) continue;
-            affinity[size_t(r)] += d == 0 ? 2 : 1;
-            heap.emplace(affinity[size_t(r)], work[size_t(band[size_t(r)])], -r);
+            if (gain[size_t(r)] == 0) touched.push_back(r);
+            gain[size_t(r)] += d == 0 ? 2 : 1;
           }
         }
+      }
+      for (const int32_t r : touched) {
+        affinity[size_t(r)] += gain[size_t(r)];
+        gain[size_t(r)] = 0;
+        heap.push(key(affinity[size_t(r)], size_t(r)));
       }
     }
     order_out.insert(order_out.end(), band.begin() + std::ptrdiff_t(head), band.end());
