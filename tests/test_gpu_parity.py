@@ -515,6 +515,80 @@ def test_k_at_the_offset_limit_goes_to_the_order_preserving_kernel():
         matrix.close()
 
 
+def values_past_2_31_case():
+    """2^15 filler block rows of 16 zero 64 x 64 blocks (exactly 2^31 values), then one block row of
+    each height with random blocks of every width, whose values start at element 2^31 (byte 8 GiB)."""
+    widths = [64, 8, 24, 40, 56, 16, 32, 48] * 8
+    filler_rows, per_row = 1 << 15, 16
+    tail_heights = [8, 24, 40, 56, 64, 16, 32, 48]
+    rows_blocks = [[8 * (j % 8) for j in range(per_row)]] * filler_rows  # width-64 columns, each twice
+    rows_blocks = rows_blocks + [[(r * 7 + j * 5) % len(widths) for j in range(5)] for r in range(len(tail_heights))]
+    row_size = np.array([64] * filler_rows + tail_heights, dtype=np.int32)
+    col_size = np.array(widths, dtype=np.int32)
+    row_ptr = np.concatenate([[0], np.cumsum([len(b) for b in rows_blocks])])
+    block_col = np.fromiter((c for b in rows_blocks for c in b), dtype=np.int32, count=int(row_ptr[-1]))
+    owners = np.repeat(np.arange(len(row_size)), np.diff(row_ptr))
+    value_off = np.concatenate([[0], np.cumsum(row_size[owners].astype(np.int64) * col_size[block_col])])
+    first_tail_block = filler_rows * per_row
+    assert value_off[first_tail_block] == 1 << 31
+    values = np.zeros(int(value_off[-1]), dtype=np.float32)  # untouched zero pages until copied
+    values[1 << 31:] = np.random.default_rng(5).uniform(-1, 1, len(values) - (1 << 31)).astype(np.float32)
+    row_scalar_off = np.concatenate([[0], np.cumsum(row_size)])
+    col_scalar_off = np.concatenate([[0], np.cumsum(col_size)])
+    host = vb.HostMatrix(len(row_size), len(col_size), row_ptr=row_ptr, block_col=block_col, row_size=row_size,
+                         col_size=col_size, row_scalar_off=row_scalar_off, col_scalar_off=col_scalar_off,
+                         value_off=value_off, values=values)
+    # The tail rows on their own, for the oracle.
+    tail = vb.HostMatrix(len(tail_heights), len(col_size), row_ptr=row_ptr[filler_rows:] - first_tail_block,
+                         block_col=block_col[first_tail_block:], row_size=row_size[filler_rows:], col_size=col_size,
+                         row_scalar_off=row_scalar_off[filler_rows:] - row_scalar_off[filler_rows],
+                         col_scalar_off=col_scalar_off, value_off=value_off[first_tail_block:] - (1 << 31),
+                         values=values[1 << 31:])
+    return host, tail, int(row_scalar_off[filler_rows])
+
+
+def test_values_past_2_31_use_64_bit_offsets():
+    """Blocks whose values start past element 2^31 of A: both kernels must read them through 64-bit
+    value offsets.  The filler rows' C stays exactly 0; the last rows match the oracle, and the
+    order-preserving kernel matches the fmaf emulation bit for bit."""
+    free, _ = torch.cuda.mem_get_info(DEVICE)
+    if free < 12 * 2**30:
+        pytest.skip("needs 12 GiB of free device memory")
+    note("values past 2^31: building the 8 GiB matrix")
+    host, tail, first_tail_row = values_past_2_31_case()
+    tail_oracle = as_oracle(tail)
+    matrix = vb.Matrix(host)
+    try:
+        stream = torch.cuda.Stream(device=DEVICE)
+        for rhs in (8, 16, 32, 64):
+            note(f"values past 2^31: rhs={rhs}")
+            b = o.make_random_input(host.scalar_cols * rhs, 40 + rhs)
+            b_dev = torch.from_numpy(b).to(DEVICE)
+            c_dev = torch.full((host.scalar_rows * rhs,), float("nan"), device=DEVICE)
+            torch.cuda.synchronize()
+            plan = vb.Plan(matrix, rhs)
+            with torch.cuda.stream(stream):
+                plan.execute(b_dev, c_dev, stream)
+            stream.synchronize()
+            out = c_dev.cpu().numpy().reshape(rhs, host.scalar_rows)
+            assert np.all(out[:, :first_tail_row] == 0.0), "filler rows"
+            check_against_oracle(tail, b, rhs, out[:, first_tail_row:].reshape(-1), f"plan rhs={rhs}")
+            if rhs == 8:
+                c_dev.fill_(float("nan"))
+                torch.cuda.synchronize()
+                with torch.cuda.stream(stream):
+                    vb.launch_row_owned_scalar(matrix.device_view(), b_dev, c_dev, rhs, stream)
+                stream.synchronize()
+                out = c_dev.cpu().numpy().reshape(rhs, host.scalar_rows)
+                assert np.all(out[:, :first_tail_row] == 0.0), "filler rows (scalar)"
+                expected = o.fmaf_order(tail_oracle, b, rhs).reshape(rhs, -1)
+                np.testing.assert_array_equal(out[:, first_tail_row:], expected, err_msg="scalar != fmaf emulation")
+            plan.close()
+            del b_dev, c_dev
+    finally:
+        matrix.close()
+
+
 # ---- execute is stateless: concurrent streams, graph capture ---------------
 
 def test_concurrent_executes_on_two_streams():
