@@ -101,7 +101,11 @@ typedef struct vbsr_plan vbsr_plan;               /* execution plan: reference P
 /* Message of the calling thread's most recent failure ("" if none). */
 const char* vbsr_last_error(void);
 
-/* HostMatrix::validate (vbsr.hpp:28; vbsr.cpp:29-82): same accept/reject set. */
+/* HostMatrix::validate (vbsr.hpp:28; vbsr.cpp:29-82): same accept/reject set
+ * for every view the reference's vectors can express.  A view can also carry
+ * a null array with entries or a negative length; those are rejected
+ * (VBSR_INVALID_ARGUMENT), as are scalar/value offset steps whose difference
+ * overflows int64. */
 int vbsr_validate(const vbsr_host_view* host);
 
 /* generate (vbsr.hpp:80; generator.cpp:7-88): same engine, same draw order,

@@ -1,6 +1,7 @@
 """Host side of the library (no GPU): generate, validate and the test-input
 generator, checked against the oracle bit for bit, plus the C ABI surface."""
 
+import ctypes
 import os
 import re
 import subprocess
@@ -124,6 +125,24 @@ def test_null_arguments_are_rejected_without_a_gpu():
     assert lib.vbsr_plan_launch_count(None) == 0
     lib.vbsr_matrix_destroy(None)
     lib.vbsr_plan_destroy(None)
+
+
+def test_validate_rejects_null_arrays_and_negative_lengths():
+    """The C view can carry a null array or a negative length, which the reference's vectors cannot:
+    validate rejects both instead of reading through them."""
+    lib = vb.library()
+    host = vb.generate(9, 17, 4, "high", "local", 11)
+    for name in ("row_ptr", "block_col", "row_size", "col_size", "row_scalar_off", "col_scalar_off", "value_off",
+                 "values"):
+        view = host._view()
+        setattr(view, name, None)
+        assert lib.vbsr_validate(ctypes.byref(view)) == vb.VBSR_INVALID_ARGUMENT, name
+        assert b"null array" in lib.vbsr_last_error(), name
+    for name in ("block_col_len", "values_len"):
+        view = host._view()
+        setattr(view, name, -1)
+        assert lib.vbsr_validate(ctypes.byref(view)) == vb.VBSR_INVALID_ARGUMENT, name
+    assert lib.vbsr_validate(ctypes.byref(host._view())) == vb.VBSR_OK
 
 
 def test_launchers_reject_bad_rhs_before_touching_the_gpu():

@@ -19,3 +19,16 @@ def test_schedule_program():
     assert result.returncode == 0, result.stdout + result.stderr
     assert result.stdout.strip().endswith("ALL OK")
     assert result.stdout.count("\nok ") + result.stdout.startswith("ok ") == 13
+
+
+def test_validate_fuzz_program():
+    """tests/cpp/test_validate_fuzz.cpp under AddressSanitizer and UBSan: 4000 mutated matrices;
+    validate accepts or rejects each without reading outside its arrays or overflowing, and
+    accepted mutants schedule inside the matrix."""
+    subprocess.run(["make", "-s", "-C", CPP, "test_validate_fuzz"], check=True)
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=1")
+    result = subprocess.run([os.path.join(CPP, "test_validate_fuzz")], capture_output=True, text=True, timeout=600,
+                            env=env)
+    print(result.stdout)
+    assert result.returncode == 0, result.stdout + result.stderr
+    assert result.stdout.strip().endswith("ALL OK")

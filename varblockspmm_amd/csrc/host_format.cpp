@@ -42,6 +42,13 @@ namespace {
 
 bool valid_block_extent(int32_t size) { return size >= 8 && size <= 64 && size % 8 == 0; }
 
+// True when next - prev == expected.  A difference that overflows int64 is
+// never equal (the reference's subtraction would be undefined there).
+bool step_is(int64_t prev, int64_t next, int64_t expected) {
+  int64_t difference = 0;
+  return !__builtin_sub_overflow(next, prev, &difference) && difference == expected;
+}
+
 }  // namespace
 
 // vbsr.cpp:29-82.  The checks run coarse to fine in the reference's order, so
@@ -49,6 +56,14 @@ bool valid_block_extent(int32_t size) { return size >= 8 && size <= 64 && size %
 void validate(const vbsr_host_view& m) {
   const int64_t rows = m.block_rows, cols = m.block_cols;
   if (rows <= 0 || cols <= 0) reject("positive block dimensions required");
+  // The C view can carry null arrays, which the reference's vectors cannot:
+  // any array with entries must be present.
+  if ((m.row_ptr_len > 0 && !m.row_ptr) || (m.block_col_len > 0 && !m.block_col) ||
+      (m.row_size_len > 0 && !m.row_size) || (m.col_size_len > 0 && !m.col_size) ||
+      (m.row_scalar_off_len > 0 && !m.row_scalar_off) || (m.col_scalar_off_len > 0 && !m.col_scalar_off) ||
+      (m.value_off_len > 0 && !m.value_off) || (m.values_len > 0 && !m.values) || m.block_col_len < 0 ||
+      m.values_len < 0)
+    reject("null array with entries, or a negative length");
   if (m.row_ptr_len != rows + 1 || m.row_size_len != rows || m.col_size_len != cols)
     reject("metadata size mismatch");
   if (m.row_scalar_off_len != rows + 1 || m.col_scalar_off_len != cols + 1)
@@ -62,12 +77,12 @@ void validate(const vbsr_host_view& m) {
   for (int64_t i = 0; i < rows; ++i) {
     const int32_t h = m.row_size[i];
     if (m.row_ptr[i] > m.row_ptr[i + 1] || !valid_block_extent(h) ||
-        m.row_scalar_off[i + 1] - m.row_scalar_off[i] != h)
+        !step_is(m.row_scalar_off[i], m.row_scalar_off[i + 1], h))
       reject("bad block row");
   }
   for (int64_t j = 0; j < cols; ++j) {
     const int32_t w = m.col_size[j];
-    if (!valid_block_extent(w) || m.col_scalar_off[j + 1] - m.col_scalar_off[j] != w)
+    if (!valid_block_extent(w) || !step_is(m.col_scalar_off[j], m.col_scalar_off[j + 1], w))
       reject("bad block column");
   }
 
@@ -77,7 +92,7 @@ void validate(const vbsr_host_view& m) {
     while (m.row_ptr[owner + 1] <= blk) ++owner;
     const int32_t col = m.block_col[blk];
     if (col < 0 || col >= cols) reject("block column out of range");
-    if (m.value_off[blk + 1] - m.value_off[blk] != int64_t(m.row_size[owner]) * m.col_size[col])
+    if (!step_is(m.value_off[blk], m.value_off[blk + 1], int64_t(m.row_size[owner]) * m.col_size[col]))
       reject("block payload mismatch");
   }
 }
