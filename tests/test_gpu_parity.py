@@ -175,6 +175,26 @@ def test_public_launcher_matches_plan(rhs):
     c.close()
 
 
+def test_launchers_reject_panels_of_the_wrong_size():
+    """A device panel one float short (or long) is refused before any launch, by every entry point."""
+    note("wrong-size panels")
+    rhs = 16
+    c = Case(vb.generate(40, 40, 4, "high", "random", 3), rhs, 3)
+    view, schedule = c.matrix.device_view(), c.matrix.row_schedule()
+    short_b = torch.empty(c.b.size - 1, dtype=torch.float32, device=DEVICE)
+    long_c = torch.empty(c.c_dev.numel() + 1, dtype=torch.float32, device=DEVICE)
+    plan = vb.Plan(c.matrix, rhs)
+    for b, cc in ((short_b, c.c_dev), (c.b_dev, long_c)):
+        with pytest.raises(ValueError, match="expected"):
+            vb.launch_row_owned(view, schedule, b, cc, rhs, c.stream)
+        with pytest.raises(ValueError, match="expected"):
+            vb.launch_row_owned_scalar(view, b, cc, rhs, c.stream)
+        with pytest.raises(ValueError, match="expected"):
+            plan.execute(b, cc, c.stream)
+    plan.close()
+    c.close()
+
+
 @pytest.mark.parametrize("rhs", [8, 32])
 def test_misaligned_b_takes_the_order_preserving_kernel(rhs):
     """A B panel that is only 4-byte aligned: the tuned launcher refuses it,

@@ -155,6 +155,21 @@ def test_launchers_reject_bad_rhs_before_touching_the_gpu():
             vb.launch_row_owned_scalar(view, None, None, rhs)
 
 
+def test_launchers_check_torch_panels_before_touching_the_gpu():
+    """The Python launchers check what the C ABI cannot see: a torch panel must be a contiguous
+    float32 device tensor of exactly scalar_cols * rhs (B) or scalar_rows * rhs (C) floats."""
+    torch = pytest.importorskip("torch")
+    view = vb.DeviceView()
+    view.block_rows, view.scalar_rows, view.scalar_cols = 4, 96, 80
+    host_b = torch.zeros(80 * 8)  # right size, but host memory
+    for launch in (lambda b, c: vb.launch_row_owned(view, vb.RowSchedule(), b, c, 8),
+                   lambda b, c: vb.launch_row_owned_scalar(view, b, c, 8)):
+        with pytest.raises(ValueError, match="device tensor"):
+            launch(host_b, None)
+        with pytest.raises(ValueError, match="device tensor"):
+            launch(None, torch.zeros(96 * 8, dtype=torch.float64))
+
+
 def test_csr_plan_rejects_bad_input_before_touching_the_gpu():
     host = vb.generate(4, 6, 2, "high", "random", 5)
     for rhs in (0, 12, 128):

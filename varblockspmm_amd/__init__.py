@@ -305,12 +305,16 @@ class Plan:
 
 def launch_row_owned(device_view, schedule, B, C, rhs, stream=None):
     """launch_row_owned (vbsr.hpp:158-159): the tuned kernel on a device view with its matrix's schedule."""
+    _check_panel(B, device_view.scalar_cols * int(rhs), "B")
+    _check_panel(C, device_view.scalar_rows * int(rhs), "C")
     _check(library().vbsr_launch_row_owned(ctypes.byref(device_view), ctypes.byref(schedule), _address(B),
                                            _address(C), int(rhs), _stream(stream)))
 
 
 def launch_row_owned_scalar(device_view, B, C, rhs, stream=None):
     """launch_row_owned_scalar (vbsr.hpp:161): the reference-order kernel."""
+    _check_panel(B, device_view.scalar_cols * int(rhs), "B")
+    _check_panel(C, device_view.scalar_rows * int(rhs), "C")
     _check(library().vbsr_launch_row_owned_scalar(ctypes.byref(device_view), _address(B), _address(C), int(rhs),
                                                   _stream(stream)))
 
