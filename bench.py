@@ -11,11 +11,12 @@ with hipEventDisableSystemFence: the HIP runtime's timing-only events, which
 skip the system-scope cache writeback/invalidate that a default event adds
 around the kernel (the runtime documents them as the accurate way to time on
 AMD GPUs).  The median of default events is reported beside it.
-"cold" steps first read a 1 GiB buffer (untimed, read-only so no dirty lines
-are left behind) so that neither L2 nor the 256 MB Infinity Cache holds A, B
-or C -- inputs are resident in HBM only.
-"hot" steps run back to back, the reference's methodology
-(bench/benchmark.cpp:148-183).  `value` is algorithmic bytes / cold median.
+Every step is synchronised before the next is enqueued, as the reference
+times each repetition (bench/benchmark.cpp:148-183: record, run, record,
+synchronise).  "cold" steps first read a 1 GiB buffer (untimed, read-only so
+no dirty lines are left behind) so that neither L2 nor the 256 MB Infinity
+Cache holds A, B or C -- inputs are resident in HBM only.  "hot" steps do not:
+the reference's methodology.  `value` is algorithmic bytes / cold median.
 
 Algorithmic work per execute: bytes = 4*S (A once) + 4*rhs*K (B once)
 + 4*rhs*M (C once) + metadata; flops = 2*rhs*S; S = sum of h*w.
@@ -250,6 +251,9 @@ def main():
                 record(starts[i])
                 step()
                 record(ends[i])
+                # One step at a time, as the reference times each repetition
+                # (bench/benchmark.cpp:162-167: record, run, record, sync).
+                stream.synchronize()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         return sorted(elapsed(s, e) for s, e in zip(starts, ends)), wall
@@ -345,9 +349,10 @@ def main():
         "data": "synthetic (seeded generator, B = mt19937 uniform[-1,1])",
         "config": {"workload": workload, "kernel": args.kernel, "sum_hw": work["sum_hw"],
                    "algorithmic_bytes": work["bytes"], "flops": work["flops"], "launches": plan.launch_count(),
-                   "timing": "hipEventDisableSystemFence events on the kernel's stream; cold = 1 GiB read-only "
-                             "sweep between steps (untimed); hot = back to back; default_event_median_ms = cold "
-                             "median with default (system-fenced) events"},
+                   "timing": "hipEventDisableSystemFence events on the kernel's stream, each step synchronised "
+                             "before the next (as bench/benchmark.cpp:148-183); cold = 1 GiB read-only sweep before "
+                             "each step (untimed); hot = no sweep; default_event_median_ms = cold median with default "
+                             "(system-fenced) events"},
         "roofline": {"bound": "hbm" if args.rhs <= 32 else "mfma", "achieved": round(achieved_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "kernel_avg_ms": round(mean, 5)},
