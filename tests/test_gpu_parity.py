@@ -214,6 +214,27 @@ def test_misaligned_b_takes_the_order_preserving_kernel(rhs):
     c.close()
 
 
+@pytest.mark.parametrize("rhs", [8, 32])
+def test_misaligned_c_takes_the_order_preserving_kernel(rhs):
+    """A C panel that is only 4-byte aligned (the RHS 8 kernel stores 16 bytes per lane for rows of
+    56 and 64): the tuned launcher refuses it, Plan::execute runs the order-preserving kernel."""
+    note(f"misaligned C rhs={rhs}")
+    c = Case(vb.generate(40, 40, 4, "bimodal8or64", "random", 19), rhs, 19)
+    storage = torch.full((c.c_dev.numel() + 4,), float("nan"), dtype=torch.float32, device=DEVICE)
+    shifted = storage[1:1 + c.c_dev.numel()]
+    assert shifted.data_ptr() % 16 != 0
+    view = c.matrix.device_view()
+    with pytest.raises(ValueError):
+        vb.launch_row_owned(view, c.matrix.row_schedule(), c.b_dev, shifted, rhs, c.stream)
+    plan = vb.Plan(c.matrix, rhs)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(c.stream):
+        plan.execute(c.b_dev, shifted, c.stream)
+    c.stream.synchronize()
+    np.testing.assert_array_equal(shifted.cpu().numpy(), o.fmaf_order(c.oracle, c.b, rhs))
+    c.close()
+
+
 @pytest.mark.parametrize("rhs", [8, 16, 32, 64])
 def test_infinite_b_matches_reference_semantics(rhs):
     """+Inf in one B entry: every output whose row touches it with a positive A

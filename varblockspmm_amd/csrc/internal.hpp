@@ -108,9 +108,9 @@ inline bool supported_rhs(int rhs) { return rhs == 8 || rhs == 16 || rhs == 32 |
 void launch_scalar(const vbsr_device_view& a, const float* b, float* c, int rhs, hipStream_t stream);
 
 // Row-owned MFMA kernel (row_owned_mfma.hip).  Launch count: 1 (0 for an
-// empty schedule).  Requires row_owned_supported(a, b): B 16-byte aligned and
-// fewer than 2^26 scalar columns (32-bit buffer offsets).
-bool row_owned_supported(const vbsr_device_view& a, const float* b);
+// empty schedule).  Requires row_owned_supported(a, b, c): B and C 16-byte
+// aligned and fewer than 2^26 scalar columns (32-bit buffer offsets).
+bool row_owned_supported(const vbsr_device_view& a, const float* b, const float* c);
 void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& schedule, const float* b, float* c,
                       int rhs, hipStream_t stream);
 

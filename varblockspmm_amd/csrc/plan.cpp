@@ -8,9 +8,10 @@
 // kernel and the height split has no counterpart.  The matrix's row schedule
 // (schedule.cpp) orders and places the rows instead.
 //
-// B panels that are not 16-byte aligned (the kernel's vector loads need it),
-// and matrices with 2^26 or more scalar columns (its 32-bit buffer offsets),
-// go to the order-preserving kernel, which has neither limit.
+// B or C panels that are not 16-byte aligned (the kernel's vector loads and
+// stores need it), and matrices with 2^26 or more scalar columns (its 32-bit
+// buffer offsets), go to the order-preserving kernel, which has neither
+// limit.
 #include "internal.hpp"
 
 namespace vbsr_amd {
@@ -25,7 +26,7 @@ Plan::Plan(const DeviceMatrix& matrix, const vbsr_plan_options& o)
 }
 
 void Plan::execute(const float* b, float* c, hipStream_t stream) const {
-  if (row_owned_supported(a, b))
+  if (row_owned_supported(a, b, c))
     launch_row_owned(a, schedule, b, c, options.rhs_width, stream);
   else
     launch_scalar(a, b, c, options.rhs_width, stream);
