@@ -3,7 +3,8 @@
 //   * the step records cover every block of every row exactly once, in
 //     row_ptr order, with the A and B offsets the kernel reads;
 //   * both launch orders hold every block row once, padding slots have
-//     step_count < 0, and each row item describes its row;
+//     step_count < 0, and each row item describes its row, including each
+//     wave's first step record;
 //   * both orders place each row on the same XCD (workgroup index mod 8), and
 //     no XCD's work exceeds an eighth of the total by more than one row's;
 //   * `rows` runs each XCD's rows heaviest first; `rows_wide` ends each XCD's
@@ -61,6 +62,12 @@ void check_order(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s, const
     CHECK(++seen[size_t(i)] == 1);
     CHECK(item.c_off == m.row_scalar_off[i]);
     CHECK(item.h == m.row_size[i]);
+    for (int w = 0; w < vbsr_amd::kRowWaves; ++w) {
+      const int32_t step = item.step_first + vbsr_amd::kStepRun * w;
+      const bool has = vbsr_amd::kStepRun * w < item.step_count;
+      CHECK(item.first[w].a_off == (has ? s.steps[size_t(step)].a_off : 0));
+      CHECK(item.first[w].b_off == (has ? s.steps[size_t(step)].b_off : 0));
+    }
     if (xcd_of_row[size_t(i)] < 0) xcd_of_row[size_t(i)] = xcd;
     CHECK(xcd_of_row[size_t(i)] == xcd);
     load[size_t(xcd)] += row_work(item);

@@ -49,18 +49,28 @@ struct alignas(16) StepRec {
 static_assert(sizeof(StepRec) == 16, "StepRec is read as one dwordx4");
 constexpr int64_t kHalfStep = int64_t(1) << 62;
 
+// The row-owned kernel's workgroup: kRowWaves waves share a row's k steps,
+// dealt in runs of kStepRun consecutive steps (wave w's first step is the
+// row's step kStepRun * w).
+constexpr int kRowWaves = 4;
+constexpr int kStepRun = 2;
+
 // One workgroup's work: block row `row`, whose steps are
 // steps[step_first .. step_first + step_count).  A padding slot has
-// step_count < 0.  32 bytes, read with one scalar load.
-struct alignas(16) RowItem {
+// step_count < 0.  first[w] repeats wave w's first step record (zero when
+// the wave has none), so the kernel can issue that step's loads as soon as
+// the row item arrives instead of after the step records.  96 bytes, read
+// with scalar loads.
+struct alignas(32) RowItem {
   int64_t c_off;       // row_scalar_off[row]: first row of C written
   int32_t step_first;  // index of the row's first StepRec
   int32_t step_count;  // the row's k steps; < 0 for a padding slot
   int32_t h;           // row_size[row]: leading dimension of the row's blocks
   int32_t row;         // block row (diagnostics only)
   int32_t pad0, pad1;
+  StepRec first[kRowWaves];
 };
-static_assert(sizeof(RowItem) == 32, "RowItem is read as 8 dwords");
+static_assert(sizeof(RowItem) == 96, "RowItem is read as 24 dwords");
 
 struct HostSchedule {
   std::vector<StepRec> steps;      // row after row, blocks in row_ptr order

@@ -52,8 +52,10 @@
 // faster and the A slot stays.
 //
 // Pipeline.  A wave's step records are read with one load (lane j holds its
-// j-th step).  Two register stages alternate: the loads of step j + 1 are in
-// flight while step j computes.  All lane offsets are per-row constants, so
+// j-th step); its first step's record also comes with the row item, so that
+// step's loads are issued without waiting for that load.  Two register
+// stages alternate: the loads of step j + 1 are in flight while step j
+// computes.  All lane offsets are per-row constants, so
 // a step costs its loads, its buffer resources, its LDS round trip and its
 // MFMAs.
 #include <hip/hip_runtime.h>
@@ -67,10 +69,10 @@ using f32x4 = float __attribute__((ext_vector_type(4)));
 using rsrc_t = __amdgpu_buffer_rsrc_t;
 
 constexpr int kWave = 64;
-constexpr int kWaves = 4;
+constexpr int kWaves = kRowWaves;
 constexpr int kThreads = kWave * kWaves;
 constexpr int kMaxTiles = 4;  // h <= 64
-constexpr int kRun = 2;       // consecutive steps dealt to one wave
+constexpr int kRun = kStepRun;  // consecutive steps dealt to one wave
 // Steps whose records one wave holds at once (one per lane): a row is
 // processed in segments of kWaves * kWave steps.
 constexpr int kSegment = kWaves * kWave;
@@ -133,6 +135,17 @@ __device__ __forceinline__ int owned_steps(int count, int wave) {
   const int rest = count % kRun;
   const int full_owned = full > wave ? (full - wave + kWaves - 1) / kWaves : 0;
   return full_owned * kRun + ((rest > 0 && full % kWaves == wave) ? rest : 0);
+}
+
+// The wave's first step of the row, which the row item carries (a switch
+// keeps the selection in scalar registers).
+__device__ __forceinline__ StepRec first_step(const RowItem& item, int wave) {
+  switch (wave) {
+  case 0: return item.first[0];
+  case 1: return item.first[1];
+  case 2: return item.first[2];
+  default: return item.first[3];
+  }
 }
 
 // Index within its segment of the wave's j-th step.
@@ -220,13 +233,16 @@ __device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, c
     const int mine = owned_steps(seg_count, wave);
     if (mine == 0) continue;
     const StepRec rec = L.steps[min(first + seg + owned_step(min(lane, mine - 1), wave), L.step_limit)];
+    const StepRec lead = first_step(item, wave);
 
     // Loads the wave's j-th step of the segment; a dead step (live == false)
-    // gets zero-byte resources.
+    // gets zero-byte resources.  The row's first step comes from the row item,
+    // so its loads do not wait for the step records.
     auto issue = [&](Stage<RHS, T>& st, int j, bool live) {
       const int l = min(j, kWave - 1);
-      const int64_t a_off = lane_value(rec.a_off, l);
-      const int64_t b_word = lane_value(rec.b_off, l);
+      const bool leading = seg == 0 && j == 0;
+      const int64_t a_off = leading ? lead.a_off : lane_value(rec.a_off, l);
+      const int64_t b_word = leading ? lead.b_off : lane_value(rec.b_off, l);
       const bool half = (b_word & kHalfStep) != 0;
       const rsrc_t a_rsrc = make_rsrc(L.a.values + a_off, live ? (half ? a_half_bytes : a_full_bytes) : 0u);
       // The buffer-load builtins return raw bits (u32x4): bit-cast them.

@@ -122,6 +122,8 @@ HostSchedule build_schedule(const vbsr_host_view& m) {
         item.step_count = step_first[size_t(i) + 1] - step_first[size_t(i)];
         item.h = m.row_size[i];
         item.row = i;
+        for (int w = 0; w < kRowWaves; ++w)
+          if (kStepRun * w < item.step_count) item.first[w] = out.steps[size_t(item.step_first + kStepRun * w)];
       }
     }
   };
