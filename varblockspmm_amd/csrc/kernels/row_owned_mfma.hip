@@ -8,7 +8,9 @@
 // block, or the 8 that end a block whose width is 8 mod 16; one precomputed
 // record each) are dealt to the four waves in runs of two; each wave
 // accumulates all T = ceil(h/16) row tiles for its steps, and the four
-// partial slabs are summed in LDS in a fixed order, (w0 + w2) + (w1 + w3).
+// partial slabs are summed in LDS in a fixed order, (w0 + w2) + (w1 + w3):
+// at RHS 16 and 32 by wave 0 after one barrier, at RHS 8 and 64 in pairs
+// over three barriers.
 // The accumulation order depends only on the matrix, so results are
 // bit-identical from run to run.
 //
@@ -47,7 +49,7 @@
 // four rows of block column 4 g + i are 16 contiguous bytes, read by load i
 // straight into MFMA layout; lanes past h (h = 56) hold values of the next
 // column, which only reach output rows that are never stored.  That frees
-// the registers that address the A slot, and RHS 8 runs 7 waves per SIMD
+// the registers that address the A slot, and RHS 8 runs 6 waves per SIMD
 // instead of 5 (about 2% faster); at the other widths the same path is not
 // faster and the A slot stays.
 //
@@ -102,8 +104,8 @@ constexpr int rhs_tiles() {
 }
 
 // LDS of one workgroup: one area per wave holding its B slot and its A slot.
-// The reduction's two partial slabs reuse the areas of waves 2 and 3 (whose
-// main loops are over by then), which are sized for them.
+// The reduction's partial slabs reuse the areas of the waves that leave
+// them (their main loops are over by then), which are sized for them.
 template <int RHS>
 struct Lds {
   static constexpr int kBBytes = rhs_tiles<RHS>() * kWave * 16;
@@ -114,9 +116,16 @@ struct Lds {
   static constexpr int kSlotBytes = kBBytes + kABytes;
   static constexpr int kPartialBytes = kMaxTiles * rhs_tiles<RHS>() * kWave * 16;
   static constexpr int kBigBytes = kSlotBytes > kPartialBytes ? kSlotBytes : kPartialBytes;
-  static constexpr int kTotal = 2 * kSlotBytes + 2 * kBigBytes;
+  // RHS 16 and 32 reduce in one barrier through the areas of waves 1-3, so
+  // those three are sized for a partial slab; RHS 8 and 64 reduce in three
+  // barriers through the areas of waves 2 and 3 (at RHS 64 a third large
+  // area would cost a workgroup per CU; at RHS 8 the one-barrier sum costs
+  // registers without a measurable gain).
+  static constexpr bool kOneBarrier = RHS == 16 || RHS == 32;
+  static constexpr int kSmall = kOneBarrier ? 1 : 2;  // areas that hold a slot only
+  static constexpr int kTotal = kSmall * kSlotBytes + (kWaves - kSmall) * kBigBytes;
   static __device__ __forceinline__ int area(int wave) {
-    return wave < 2 ? wave * kSlotBytes : 2 * kSlotBytes + (wave - 2) * kBigBytes;
+    return wave < kSmall ? wave * kSlotBytes : kSmall * kSlotBytes + (wave - kSmall) * kBigBytes;
   }
 };
 
@@ -303,34 +312,60 @@ __device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, c
     }
   }
 
-  // Fixed-order reduction of the four partial slabs, (w0 + w2) + (w1 + w3),
-  // through the LDS areas of waves 2 and 3.
+  // Fixed-order reduction of the four partial slabs, (w0 + w2) + (w1 + w3);
+  // afterwards wave 0's acc holds the row's sums.
+  f32x4* part1 = reinterpret_cast<f32x4*>(lds + Layout::area(1));
   f32x4* part2 = reinterpret_cast<f32x4*>(lds + Layout::area(2));
   f32x4* part3 = reinterpret_cast<f32x4*>(lds + Layout::area(3));
-  if (wave >= 2) {
-    f32x4* part = wave == 2 ? part2 : part3;
+  auto slab = [&](int t, int nt) { return (t * kRhsTiles + nt) * kWave + lane; };
+  if constexpr (Layout::kOneBarrier) {
+    // Waves 1-3 leave their slabs in their own LDS areas; wave 0 sums them.
+    if (wave > 0) {
+      f32x4* part = wave == 1 ? part1 : wave == 2 ? part2 : part3;
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int nt = 0; nt < kRhsTiles; ++nt) part[slab(t, nt)] = acc[t][nt];
+    }
+    __syncthreads();
+    if (wave != 0) return;
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
-      for (int nt = 0; nt < kRhsTiles; ++nt) part[(t * kRhsTiles + nt) * kWave + lane] = acc[t][nt];
-  }
-  __syncthreads();
-  if (wave < 2) {
-    const f32x4* part = wave == 0 ? part2 : part3;
+      for (int nt = 0; nt < kRhsTiles; ++nt)
+        acc[t][nt] = (acc[t][nt] + part2[slab(t, nt)]) + (part1[slab(t, nt)] + part3[slab(t, nt)]);
+  } else {
+    // Waves 2 and 3 leave their slabs; waves 0 and 1 add them; wave 1 passes
+    // its sum to wave 0 through wave 2's area.
+    if (wave >= 2) {
+      f32x4* part = wave == 2 ? part2 : part3;
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int nt = 0; nt < kRhsTiles; ++nt) part[slab(t, nt)] = acc[t][nt];
+    }
+    __syncthreads();
+    if (wave < 2) {
+      const f32x4* part = wave == 0 ? part2 : part3;
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int nt = 0; nt < kRhsTiles; ++nt) acc[t][nt] += part[slab(t, nt)];
+    }
+    __syncthreads();
+    if (wave == 1) {
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int nt = 0; nt < kRhsTiles; ++nt) part2[slab(t, nt)] = acc[t][nt];
+    }
+    __syncthreads();
+    if (wave != 0) return;
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
-      for (int nt = 0; nt < kRhsTiles; ++nt) acc[t][nt] += part[(t * kRhsTiles + nt) * kWave + lane];
+      for (int nt = 0; nt < kRhsTiles; ++nt) acc[t][nt] += part2[slab(t, nt)];
   }
-  __syncthreads();
-  if (wave == 1) {
-#pragma unroll
-    for (int t = 0; t < T; ++t)
-#pragma unroll
-      for (int nt = 0; nt < kRhsTiles; ++nt) part2[(t * kRhsTiles + nt) * kWave + lane] = acc[t][nt];
-  }
-  __syncthreads();
-  if (wave != 0) return;
   const int64_t ldc = L.a.scalar_rows;
   if constexpr (kDirect) {
     // Lane x holds rows 4 x .. 4 x + 3 of output columns 4 g + v: one
@@ -340,7 +375,7 @@ __device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, c
       float* c_rows = L.c + item.c_off + 4 * x;
       f32x4 sum[T];
 #pragma unroll
-      for (int t = 0; t < T; ++t) sum[t] = acc[t][0] + part2[t * kWave + lane];
+      for (int t = 0; t < T; ++t) sum[t] = acc[t][0];
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int n = 4 * group + v;
@@ -356,7 +391,7 @@ __device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, c
     if (t < T - 1 || x < last_rows) {
 #pragma unroll
       for (int nt = 0; nt < kRhsTiles; ++nt) {
-        const f32x4 sum = acc[t][nt] + part2[(t * kRhsTiles + nt) * kWave + lane];
+        const f32x4 sum = acc[t][nt];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int n = nt * 16 + 4 * group + v;
