@@ -145,6 +145,15 @@ def test_validate_rejects_null_arrays_and_negative_lengths():
     assert lib.vbsr_validate(ctypes.byref(host._view())) == vb.VBSR_OK
 
 
+def test_reciprocal_division_used_by_the_mfma_kernel_is_exact():
+    """row_owned_mfma.hip finds the block column of each loaded float as (f * ceil(2^16 / h)) >> 16
+    instead of f / h: exact for every float index f < 1024 of a step and every block height."""
+    for h in range(8, 65, 8):
+        recip = -(-65536 // h)
+        f = np.arange(1024, dtype=np.uint64)
+        np.testing.assert_array_equal((f * recip) >> 16, f // h, err_msg=f"h={h}")
+
+
 def test_launchers_reject_bad_rhs_before_touching_the_gpu():
     view = vb.DeviceView()
     view.block_rows = 4

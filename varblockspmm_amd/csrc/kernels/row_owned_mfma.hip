@@ -206,11 +206,15 @@ __device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, c
   // A slot positions of this lane's loaded floats.  Lanes past the tile
   // (h = 8 mod 16) hold zeros and write them to the slot's padding (rows
   // 16 T .. 16 T + 3 of column lane & 15), which is never read.
+  // f / h is computed as (f * ceil(2^16 / h)) >> 16, which is exact for
+  // f < 1024 and h a multiple of 8 up to 64 (one uniform division per row
+  // instead of T per lane).
+  const uint32_t h_recip = uint32_t(uniform(int((65536u + uint32_t(h) - 1u) / uint32_t(h))));
   int a_write[T];
 #pragma unroll
   for (int q = 0; q < T; ++q) {
     const int f = 256 * q + 4 * lane;
-    const int k = f / h;
+    const int k = int((uint32_t(f) * h_recip) >> 16);
     a_write[q] = f < 16 * h ? k * ld + (f - k * h) : (lane & 15) * ld + 16 * T;
   }
   // MFMA-layout reads: row 16 t + x of column 4 g + i; rows past h read a
