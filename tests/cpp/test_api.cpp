@@ -181,6 +181,72 @@ void run_case(vbsr::Distribution distribution, int degree, int rhs, bool local, 
   hip_ok(hipStreamDestroy(stream), "hipStreamDestroy");
 }
 
+// Matrix is move-only (reference vbsr.cpp:128-162), and a Plan keeps a
+// non-owning view of the device arrays (reference vbsr.hpp:114-116).  A move
+// hands those arrays over without copying them, so a plan built before the
+// move keeps working; the moved-from object holds nothing, rejects use with
+// std::invalid_argument, and is destroyed harmlessly.  Move assignment frees
+// the target's own arrays first; self-assignment keeps them.
+void run_move_tests() {
+  vbsr::GeneratorOptions options;
+  options.block_rows = 9;
+  options.block_cols = 17;
+  options.degree = 4;
+  options.seed = 5;
+  const vbsr::HostMatrix host = vbsr::generate(options);
+  options.seed = 6;
+  const vbsr::HostMatrix other = vbsr::generate(options);
+  const int rhs = 32;
+  const orc_view ov = oracle_view(host);
+  std::vector<float> input(size_t(host.scalar_cols() * rhs));
+  orc_make_random_input(int64_t(input.size()), 5, input.data());
+  std::vector<float> reference(size_t(host.scalar_rows() * rhs));
+  std::vector<double> bound(reference.size());
+  orc_cpu_reference(&ov, input.data(), int64_t(input.size()), rhs, reference.data());
+  orc_abs_product_sum(&ov, input.data(), int64_t(input.size()), rhs, bound.data());
+  DeviceBuffer b(input.size()), c(reference.size());
+  hip_ok(hipMemcpy(b.ptr, input.data(), input.size() * sizeof(float), hipMemcpyHostToDevice), "upload B");
+
+  const auto run = [&](const vbsr::Plan& plan, const char* name) {
+    c.poison();
+    plan.execute(b.ptr, c.ptr);
+    hip_ok(hipDeviceSynchronize(), "sync");
+    compare(c.read(), reference, bound, name);
+  };
+  const auto require = [](bool ok, const char* failure) {
+    if (!ok) throw std::runtime_error(failure);
+  };
+
+  vbsr::Matrix first(host);
+  const float* values = first.device_view().values;
+  const vbsr::Plan before(first, {rhs, vbsr::Kernel::RowOwned});
+
+  vbsr::Matrix second(std::move(first));
+  require(first.handle() == nullptr, "moved-from Matrix still owns a handle");
+  require(first.scalar_rows() == 0 && first.scalar_cols() == 0, "moved-from Matrix reports a shape");
+  require(second.device_view().values == values, "move construction copied the device arrays");
+  require(second.scalar_rows() == host.scalar_rows() && second.scalar_cols() == host.scalar_cols(),
+          "moved-to Matrix lost its shape");
+  expect_invalid_argument([&] { (void)first.device_view(); }, "moved-from Matrix gave a device view");
+  expect_invalid_argument([&] { vbsr::Plan plan(first, {rhs, vbsr::Kernel::RowOwned}); },
+                          "Plan accepted a moved-from Matrix");
+  run(before, "plan built before a move construction");
+
+  vbsr::Matrix third(other);
+  third = std::move(second);
+  require(second.handle() == nullptr, "move-assigned-from Matrix still owns a handle");
+  require(third.device_view().values == values, "move assignment copied the device arrays");
+  vbsr::Matrix& alias = third;
+  third = std::move(alias);
+  require(third.device_view().values == values, "self move assignment dropped the device arrays");
+  run(before, "plan built before a move assignment");
+  run(vbsr::Plan(third, {rhs, vbsr::Kernel::RowOwned}), "plan built on a move-assigned Matrix");
+
+  first = std::move(third);  // a moved-from object can be assigned to again
+  require(third.handle() == nullptr && first.device_view().values == values, "second move assignment failed");
+  run(before, "plan built before two moves");
+}
+
 // tests/test_main.cpp:145-161
 int run_parameter_matrix() {
   const vbsr::Distribution distributions[] = {vbsr::Distribution::Uniform, vbsr::Distribution::LowVariance,
@@ -204,8 +270,9 @@ int run_parameter_matrix() {
 int main() {
   try {
     run_negative_tests();
+    run_move_tests();
     const int cases = run_parameter_matrix();
-    std::cout << "PASS: negative tests + " << cases
+    std::cout << "PASS: negative tests + Matrix move and lifetime tests + " << cases
               << " parameter cases (MFMA plan + order-preserving kernel + rocSPARSE CSR plan + grouped "
                  "rocBLAS plan, non-default stream, NaN-poisoned C, bit-identical repeats)\n";
     return 0;
