@@ -20,7 +20,9 @@
  *
  * Execution: vbsr_plan_execute and the launchers only enqueue kernels on the
  * given stream; they never synchronise, never allocate and use no workspace.
- * B and C must not alias.  C is fully overwritten.  Results are bit-identical
+ * B (K x N floats) and C (M x N floats) must be non-null and must not overlap;
+ * both are checked on the host before any launch (VBSR_INVALID_ARGUMENT
+ * otherwise).  C is fully overwritten.  Results are bit-identical
  * from run to run (no atomics, fixed accumulation order).
  */
 #ifndef VARBLOCKSPMM_AMD_VBSR_H

@@ -13,7 +13,9 @@
 //   * matrices whose rows share few block columns (every row on the same 8
 //     columns; rows overlapping in 15 of 16 columns) build in seconds: the
 //     chained order's work does not grow with the square of a column's users.
-// Prints one line per matrix and exits non-zero if any check fails.
+// It also checks the launchers' host-side panel check (check_panels) at the
+// edges of the B and C ranges, where no address is ever dereferenced.
+// Prints one line per check group and exits non-zero if any check fails.
 #include <algorithm>
 #include <chrono>
 #include <cstdio>
@@ -199,6 +201,36 @@ vbsr_amd::HostMatrix with_empty_row() {
   return h;
 }
 
+// B holds K x rhs floats and C M x rhs: ranges that touch are accepted,
+// ranges that share one float are not.
+void check_panel_ranges() {
+  const int before = failures;
+  vbsr_device_view v{};
+  v.scalar_rows = 96;
+  v.scalar_cols = 80;
+  const int rhs = 8;
+  static float arena[4096];
+  float* b = arena + 1024;
+  const auto rejected = [&](const float* bb, const float* cc) {
+    try {
+      vbsr_amd::check_panels(v, bb, cc, rhs);
+    } catch (const std::invalid_argument&) {
+      return true;
+    }
+    return false;
+  };
+  [&] {
+    CHECK(!rejected(b, b + 80 * rhs));      // C starts where B ends
+    CHECK(!rejected(b, b - 96 * rhs));      // C ends where B starts
+    CHECK(rejected(b, b + 80 * rhs - 1));   // C starts on B's last float
+    CHECK(rejected(b, b - 96 * rhs + 1));   // C ends on B's first float
+    CHECK(rejected(b, b));
+    CHECK(rejected(nullptr, b));
+    CHECK(rejected(b, nullptr));
+  }();
+  std::printf("%s panel ranges\n", failures == before ? "ok" : "FAILED");
+}
+
 }  // namespace
 
 int main() {
@@ -234,6 +266,7 @@ int main() {
   check_host(with_empty_row(), "hand-made, empty middle row");
   check_shared_columns(16384, 8, 8);
   check_shared_columns(65536, 16384, 16);
+  check_panel_ranges();
   std::printf("%s\n", failures == 0 ? "ALL OK" : "FAILURES");
   return failures == 0 ? 0 : 1;
 }

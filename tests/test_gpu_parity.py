@@ -195,6 +195,38 @@ def test_launchers_reject_panels_of_the_wrong_size():
     c.close()
 
 
+def test_entry_points_reject_overlapping_panels():
+    """A C panel that shares memory with B is refused before any launch, by every entry point (the
+    reference's B and C are __restrict__, row_owned.cu:12-13)."""
+    note("overlapping panels")
+    rhs = 16
+    c = Case(vb.generate(40, 40, 4, "high", "random", 3), rhs, 3)
+    view, schedule = c.matrix.device_view(), c.matrix.row_schedule()
+    b_count, c_count = c.b.size, c.c_dev.numel()
+    storage = torch.zeros(b_count + c_count, dtype=torch.float32, device=DEVICE)
+    b = storage[:b_count]
+    overlapping_c = storage[b_count - 4:b_count - 4 + c_count]
+    plan = vb.Plan(c.matrix, rhs)
+    for run in (lambda: vb.launch_row_owned(view, schedule, b, overlapping_c, rhs, c.stream),
+                lambda: vb.launch_row_owned_scalar(view, b, overlapping_c, rhs, c.stream),
+                lambda: plan.execute(b, overlapping_c, c.stream)):
+        with pytest.raises(ValueError, match="overlap"):
+            run()
+    with pytest.raises(ValueError, match="device pointers"):
+        plan.execute(None, c.c_dev, c.stream)
+    # The same storage split without overlap runs, and matches the oracle.
+    touching_c = storage[b_count:]
+    b.copy_(c.b_dev)
+    touching_c.fill_(float("nan"))
+    torch.cuda.synchronize()
+    with torch.cuda.stream(c.stream):
+        plan.execute(b, touching_c, c.stream)
+    c.stream.synchronize()
+    c.check_tolerance(touching_c.cpu().numpy(), "C right after B in one allocation")
+    plan.close()
+    c.close()
+
+
 @pytest.mark.parametrize("rhs", [8, 32])
 def test_misaligned_b_takes_the_order_preserving_kernel(rhs):
     """A B panel that is only 4-byte aligned: the tuned launcher refuses it,

@@ -164,6 +164,27 @@ def test_launchers_reject_bad_rhs_before_touching_the_gpu():
             vb.launch_row_owned_scalar(view, None, None, rhs)
 
 
+def test_launchers_reject_null_and_overlapping_panels_before_touching_the_gpu():
+    """The C ABI refuses a null B or C, and a C whose range (scalar_rows * rhs floats) meets B's
+    (scalar_cols * rhs floats): C is written while B is read.  Addresses here are never
+    dereferenced; every call is refused on the host."""
+    view = vb.DeviceView()
+    view.block_rows, view.scalar_rows, view.scalar_cols = 4, 96, 80
+    rhs = 8
+    b = 0x7f0000000000
+    b_end = b + 80 * rhs * 4
+    launchers = (lambda bb, cc: vb.launch_row_owned(view, vb.RowSchedule(), bb, cc, rhs),
+                 lambda bb, cc: vb.launch_row_owned_scalar(view, bb, cc, rhs))
+    for launch in launchers:
+        for bb, cc in ((None, b_end), (b, None), (None, None)):
+            with pytest.raises(ValueError, match="device pointers"):
+                launch(bb, cc)
+        # C starting inside B, C ending inside B, C equal to B, C covering B.
+        for cc in (b_end - 4, b - 96 * rhs * 4 + 4, b, b - 256):
+            with pytest.raises(ValueError, match="overlap"):
+                launch(b, cc)
+
+
 def test_launchers_check_torch_panels_before_touching_the_gpu():
     """The Python launchers check what the C ABI cannot see: a torch panel must be a contiguous
     float32 device tensor of exactly scalar_cols * rhs (B) or scalar_rows * rhs (C) floats."""

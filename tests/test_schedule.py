@@ -3,7 +3,8 @@ sources (varblockspmm_amd/csrc/schedule.cpp, host_format.cpp), on generated and 
 It checks the step records against the block metadata, that both launch orders (RHS 8/16 and
 RHS 32/64) are permutations of the block rows on the same XCDs with bounded work per XCD, the
 orders within each XCD, determinism, and that matrices whose rows share few block columns are
-scheduled in seconds."""
+scheduled in seconds.  It also checks the launchers' host-side panel check at the edges of the B
+and C ranges."""
 
 import os
 import subprocess
@@ -18,7 +19,7 @@ def test_schedule_program():
     print(result.stdout)
     assert result.returncode == 0, result.stdout + result.stderr
     assert result.stdout.strip().endswith("ALL OK")
-    assert result.stdout.count("\nok ") + result.stdout.startswith("ok ") == 13
+    assert result.stdout.count("\nok ") + result.stdout.startswith("ok ") == 14
 
 
 def test_validate_fuzz_program():

@@ -114,6 +114,20 @@ private:
 // True for the RHS widths the reference supports (plan.cpp:9-12).
 inline bool supported_rhs(int rhs) { return rhs == 8 || rhs == 16 || rhs == 32 || rhs == 64; }
 
+// B (K x rhs) and C (M x rhs) must be device pointers whose ranges do not
+// overlap: C is written while B is read (the reference's __restrict__
+// contract, row_owned.cu:12-13).  Checked on the host before every launch,
+// so a null or aliased panel is an invalid argument, not a device fault or
+// corrupted output.
+inline void check_panels(const vbsr_device_view& a, const float* b, const float* c, int rhs) {
+  if (b == nullptr || c == nullptr) throw std::invalid_argument("B and C must be device pointers");
+  const uintptr_t b0 = reinterpret_cast<uintptr_t>(b);
+  const uintptr_t c0 = reinterpret_cast<uintptr_t>(c);
+  const uintptr_t b1 = b0 + uintptr_t(a.scalar_cols) * uintptr_t(rhs) * sizeof(float);
+  const uintptr_t c1 = c0 + uintptr_t(a.scalar_rows) * uintptr_t(rhs) * sizeof(float);
+  if (b0 < c1 && c0 < b1) throw std::invalid_argument("B and C overlap");
+}
+
 // Order-preserving kernel (row_owned_scalar.hip).
 void launch_scalar(const vbsr_device_view& a, const float* b, float* c, int rhs, hipStream_t stream);
 

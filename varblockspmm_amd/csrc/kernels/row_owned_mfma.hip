@@ -439,6 +439,7 @@ bool row_owned_supported(const vbsr_device_view& a, const float* b, const float*
 void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& s, const float* b, float* c, int rhs,
                       hipStream_t stream) {
   if (!supported_rhs(rhs)) throw std::invalid_argument("unsupported rhs width");
+  check_panels(a, b, c, rhs);
   if (!row_owned_supported(a, b, c))
     throw std::invalid_argument("row-owned kernel needs 16-byte aligned B and C and fewer than 2^26 scalar columns");
   if (s.groups <= 0) return;

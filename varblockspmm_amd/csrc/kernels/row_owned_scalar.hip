@@ -53,6 +53,7 @@ void launch(const vbsr_device_view& a, const float* b, float* c, hipStream_t str
 
 void launch_scalar(const vbsr_device_view& a, const float* b, float* c, int rhs, hipStream_t stream) {
   if (!supported_rhs(rhs)) throw std::invalid_argument("unsupported rhs width");
+  check_panels(a, b, c, rhs);
   if (a.block_rows <= 0) return;
   switch (rhs) {
   case 8: launch<8>(a, b, c, stream); break;
