@@ -428,11 +428,12 @@ void launch(const Launch& L, int64_t groups, hipStream_t stream) {
 
 }  // namespace
 
-bool row_owned_supported(const vbsr_device_view& a, const float* b, const float* c) {
-  // 16-byte B loads and (RHS 8, four-tile rows) C stores; 32-bit buffer
-  // offsets: a B tile spans 15 columns of ld K plus one step, and must stay
-  // below the out-of-range offset.
-  return reinterpret_cast<uintptr_t>(b) % 16 == 0 && reinterpret_cast<uintptr_t>(c) % 16 == 0 &&
+bool row_owned_supported(const vbsr_device_view& a, const float* b, const float* c, int rhs) {
+  // 16-byte B loads; 16-byte C stores at RHS 8 (four-tile rows), 4-byte ones
+  // at the other widths; 32-bit buffer offsets: a B tile spans 15 columns of
+  // ld K plus one step, and must stay below the out-of-range offset.
+  const uintptr_t c_align = rhs == 8 ? 16 : 4;
+  return reinterpret_cast<uintptr_t>(b) % 16 == 0 && reinterpret_cast<uintptr_t>(c) % c_align == 0 &&
          a.scalar_cols < (int64_t(1) << 26);
 }
 
@@ -440,8 +441,10 @@ void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& s, con
                       hipStream_t stream) {
   if (!supported_rhs(rhs)) throw std::invalid_argument("unsupported rhs width");
   check_panels(a, b, c, rhs);
-  if (!row_owned_supported(a, b, c))
-    throw std::invalid_argument("row-owned kernel needs 16-byte aligned B and C and fewer than 2^26 scalar columns");
+  if (!row_owned_supported(a, b, c, rhs))
+    throw std::invalid_argument(
+        "row-owned kernel needs a 16-byte aligned B, a 16-byte aligned C at rhs 8 (4-byte at other widths) "
+        "and fewer than 2^26 scalar columns");
   if (s.groups <= 0) return;
   if (s.groups > int64_t(0x7fffffff)) throw std::invalid_argument("schedule too large for one launch");
   const void* rows = rhs >= 32 && s.rows_wide != nullptr ? s.rows_wide : s.rows;

@@ -8,10 +8,11 @@
 // kernel and the height split has no counterpart.  The matrix's row schedule
 // (schedule.cpp) orders and places the rows instead.
 //
-// B or C panels that are not 16-byte aligned (the kernel's vector loads and
-// stores need it), and matrices with 2^26 or more scalar columns (its 32-bit
-// buffer offsets), go to the order-preserving kernel, which has neither
-// limit.
+// A B panel that is not 16-byte aligned (the kernel's vector loads need it),
+// a C panel that is not 16-byte aligned at RHS 8 (vector stores there) or not
+// 4-byte aligned at other widths, and matrices with 2^26 or more scalar
+// columns (its 32-bit buffer offsets) go to the order-preserving kernel,
+// which has none of these limits.
 #include "internal.hpp"
 
 namespace vbsr_amd {
@@ -26,7 +27,7 @@ Plan::Plan(const DeviceMatrix& matrix, const vbsr_plan_options& o)
 }
 
 void Plan::execute(const float* b, float* c, hipStream_t stream) const {
-  if (row_owned_supported(a, b, c))
+  if (row_owned_supported(a, b, c, options.rhs_width))
     launch_row_owned(a, schedule, b, c, options.rhs_width, stream);
   else
     launch_scalar(a, b, c, options.rhs_width, stream);
