@@ -20,9 +20,9 @@
  *
  * Execution: vbsr_plan_execute and the launchers only enqueue kernels on the
  * given stream; they never synchronise, never allocate and use no workspace.
- * B (K x N floats) and C (M x N floats) must be non-null and must not overlap;
- * both are checked on the host before any launch (VBSR_INVALID_ARGUMENT
- * otherwise).  C is fully overwritten.  Results are bit-identical
+ * B (K x N floats) and C (M x N floats) must be non-null, 4-byte aligned and
+ * must not overlap; all three are checked on the host before any launch
+ * (VBSR_INVALID_ARGUMENT otherwise).  C is fully overwritten.  Results are bit-identical
  * from run to run (no atomics, fixed accumulation order).
  */
 #ifndef VARBLOCKSPMM_AMD_VBSR_H
@@ -163,10 +163,9 @@ int vbsr_plan_launch_count(const vbsr_plan* plan);
 /* launch_row_owned (vbsr.hpp:158-159; row_owned.cu:397-423): the tuned
  * row-owned kernel for `rhs` over `matrix`, scheduled by `schedule` (from
  * vbsr_matrix_row_schedule of the matrix that `matrix` views; the reference
- * passes row_shape_order/small/large in the same role).  B must be 16-byte
- * aligned, C 16-byte aligned at rhs 8 and 4-byte aligned at other widths, and
- * K below 2^26 (VBSR_INVALID_ARGUMENT otherwise; vbsr_plan_execute accepts
- * any alignment and K). */
+ * passes row_shape_order/small/large in the same role).  C must be 16-byte
+ * aligned at rhs 8, and K below 2^26 (VBSR_INVALID_ARGUMENT otherwise;
+ * vbsr_plan_execute takes any 4-byte aligned C and any K). */
 int vbsr_launch_row_owned(const vbsr_device_view* matrix, const vbsr_row_schedule* schedule,
                           const float* B, float* C, int32_t rhs, hipStream_t stream);
 

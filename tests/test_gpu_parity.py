@@ -227,22 +227,25 @@ def test_entry_points_reject_overlapping_panels():
     c.close()
 
 
-@pytest.mark.parametrize("rhs", [8, 32])
-def test_misaligned_b_takes_the_order_preserving_kernel(rhs):
-    """A B panel that is only 4-byte aligned: the tuned launcher refuses it,
-    Plan::execute runs the order-preserving kernel (bit-exact fmaf order)."""
+@pytest.mark.parametrize("rhs", [8, 16, 32, 64])
+def test_misaligned_b_stays_on_the_mfma_kernel(rhs):
+    """B panels 4, 8 and 12 bytes past a 16-byte boundary: the tuned kernel loads them 4 bytes at a
+    time, through the launcher and Plan::execute, with the same bits as an aligned B."""
     note(f"misaligned B rhs={rhs}")
-    c = Case(vb.generate(40, 40, 4, "high", "random", 9), rhs, 9)
-    storage = torch.empty(c.b.size + 4, dtype=torch.float32, device=DEVICE)
-    storage[1:1 + c.b.size].copy_(c.b_dev)
-    shifted = storage[1:1 + c.b.size]
-    assert shifted.data_ptr() % 16 != 0
-    view = c.matrix.device_view()
-    with pytest.raises(ValueError):
-        vb.launch_row_owned(view, c.matrix.row_schedule(), shifted, c.c_dev, rhs, c.stream)
+    c = Case(vb.generate(40, 40, 4, "bimodal8or64", "random", 9), rhs, 9)
     plan = vb.Plan(c.matrix, rhs)
-    result = c.run(lambda: plan.execute(shifted, c.c_dev, c.stream))
-    np.testing.assert_array_equal(result, o.fmaf_order(c.oracle, c.b, rhs))
+    aligned = c.run_plan(plan)
+    c.check_tolerance(aligned, "aligned B")
+    view, schedule = c.matrix.device_view(), c.matrix.row_schedule()
+    for shift in (1, 2, 3):
+        storage = torch.empty(c.b.size + 4, dtype=torch.float32, device=DEVICE)
+        shifted = storage[shift:shift + c.b.size]
+        shifted.copy_(c.b_dev)
+        assert shifted.data_ptr() % 16 == 4 * shift
+        np.testing.assert_array_equal(c.run(lambda: plan.execute(shifted, c.c_dev, c.stream)), aligned)
+        np.testing.assert_array_equal(
+            c.run(lambda: vb.launch_row_owned(view, schedule, shifted, c.c_dev, rhs, c.stream)), aligned)
+    plan.close()
     c.close()
 
 

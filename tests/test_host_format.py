@@ -165,8 +165,8 @@ def test_launchers_reject_bad_rhs_before_touching_the_gpu():
 
 
 def test_launchers_reject_null_and_overlapping_panels_before_touching_the_gpu():
-    """The C ABI refuses a null B or C, and a C whose range (scalar_rows * rhs floats) meets B's
-    (scalar_cols * rhs floats): C is written while B is read.  Addresses here are never
+    """The C ABI refuses a null B or C, a B or C that is not 4-byte aligned, and a C whose range
+    (scalar_rows * rhs floats) meets B's (scalar_cols * rhs floats): C is written while B is read.  Addresses here are never
     dereferenced; every call is refused on the host."""
     view = vb.DeviceView()
     view.block_rows, view.scalar_rows, view.scalar_cols = 4, 96, 80
@@ -178,6 +178,9 @@ def test_launchers_reject_null_and_overlapping_panels_before_touching_the_gpu():
     for launch in launchers:
         for bb, cc in ((None, b_end), (b, None), (None, None)):
             with pytest.raises(ValueError, match="device pointers"):
+                launch(bb, cc)
+        for bb, cc in ((b + 2, b_end), (b, b_end + 2)):
+            with pytest.raises(ValueError, match="4-byte aligned"):
                 launch(bb, cc)
         # C starting inside B, C ending inside B, C equal to B, C covering B.
         for cc in (b_end - 4, b - 96 * rhs * 4 + 4, b, b - 256):

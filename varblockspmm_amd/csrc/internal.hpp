@@ -114,15 +114,17 @@ private:
 // True for the RHS widths the reference supports (plan.cpp:9-12).
 inline bool supported_rhs(int rhs) { return rhs == 8 || rhs == 16 || rhs == 32 || rhs == 64; }
 
-// B (K x rhs) and C (M x rhs) must be device pointers whose ranges do not
-// overlap: C is written while B is read (the reference's __restrict__
-// contract, row_owned.cu:12-13).  Checked on the host before every launch,
-// so a null or aliased panel is an invalid argument, not a device fault or
-// corrupted output.
+// B (K x rhs) and C (M x rhs) must be float-aligned device pointers whose
+// ranges do not overlap: C is written while B is read (the reference's
+// __restrict__ contract, row_owned.cu:12-13).  Checked on the host before
+// every launch, so a null, misaligned or aliased panel is an invalid
+// argument, not a device fault or corrupted output.
 inline void check_panels(const vbsr_device_view& a, const float* b, const float* c, int rhs) {
   if (b == nullptr || c == nullptr) throw std::invalid_argument("B and C must be device pointers");
   const uintptr_t b0 = reinterpret_cast<uintptr_t>(b);
   const uintptr_t c0 = reinterpret_cast<uintptr_t>(c);
+  if (b0 % alignof(float) != 0 || c0 % alignof(float) != 0)
+    throw std::invalid_argument("B and C must be 4-byte aligned");
   const uintptr_t b1 = b0 + uintptr_t(a.scalar_cols) * uintptr_t(rhs) * sizeof(float);
   const uintptr_t c1 = c0 + uintptr_t(a.scalar_rows) * uintptr_t(rhs) * sizeof(float);
   if (b0 < c1 && c0 < b1) throw std::invalid_argument("B and C overlap");
@@ -132,9 +134,10 @@ inline void check_panels(const vbsr_device_view& a, const float* b, const float*
 void launch_scalar(const vbsr_device_view& a, const float* b, float* c, int rhs, hipStream_t stream);
 
 // Row-owned MFMA kernel (row_owned_mfma.hip).  Launch count: 1 (0 for an
-// empty schedule).  Requires row_owned_supported(a, b, c, rhs): B 16-byte
-// aligned, C 16-byte aligned at rhs 8 and 4-byte aligned otherwise, and
-// fewer than 2^26 scalar columns (32-bit buffer offsets).
+// empty schedule).  Requires row_owned_supported(a, b, c, rhs): B 4-byte
+// aligned (16-byte aligned B takes 16-byte loads), C 16-byte aligned at rhs 8
+// and 4-byte aligned otherwise, and fewer than 2^26 scalar columns (32-bit
+// buffer offsets).
 bool row_owned_supported(const vbsr_device_view& a, const float* b, const float* c, int rhs);
 void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& schedule, const float* b, float* c,
                       int rhs, hipStream_t stream);

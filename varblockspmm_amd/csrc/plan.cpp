@@ -8,11 +8,11 @@
 // kernel and the height split has no counterpart.  The matrix's row schedule
 // (schedule.cpp) orders and places the rows instead.
 //
-// A B panel that is not 16-byte aligned (the kernel's vector loads need it),
-// a C panel that is not 16-byte aligned at RHS 8 (vector stores there) or not
-// 4-byte aligned at other widths, and matrices with 2^26 or more scalar
-// columns (its 32-bit buffer offsets) go to the order-preserving kernel,
-// which has none of these limits.
+// A C panel that is not 16-byte aligned at RHS 8 (the kernel's vector
+// stores there need it), and matrices with 2^26 or more scalar columns (its
+// 32-bit buffer offsets), go to the order-preserving kernel, which has
+// neither limit.  A B panel that is not 16-byte aligned stays on the MFMA
+// kernel, which then loads B 4 bytes at a time.
 #include "internal.hpp"
 
 namespace vbsr_amd {
