@@ -264,29 +264,11 @@ def run_into(c, launch):
     c.stream.synchronize()
 
 
-def test_misaligned_c_at_rhs_8_takes_the_order_preserving_kernel():
-    """At RHS 8 the tuned kernel stores 16 bytes per lane for rows of 56 and 64, so a C panel that
-    is only 4-byte aligned is refused by the tuned launcher and Plan::execute runs the
-    order-preserving kernel."""
-    note("misaligned C rhs=8")
-    rhs = 8
-    c = Case(vb.generate(40, 40, 4, "bimodal8or64", "random", 19), rhs, 19)
-    storage, shifted = misaligned_c(c)
-    view = c.matrix.device_view()
-    with pytest.raises(ValueError):
-        vb.launch_row_owned(view, c.matrix.row_schedule(), c.b_dev, shifted, rhs, c.stream)
-    plan = vb.Plan(c.matrix, rhs)
-    run_into(c, lambda: plan.execute(c.b_dev, shifted, c.stream))
-    np.testing.assert_array_equal(shifted.cpu().numpy(), o.fmaf_order(c.oracle, c.b, rhs))
-    assert torch.isnan(storage[0]) and torch.isnan(storage[1 + c.c_dev.numel():]).all()
-    c.close()
-
-
-@pytest.mark.parametrize("rhs", [16, 32, 64])
-def test_misaligned_c_at_wider_rhs_stays_on_the_mfma_kernel(rhs):
-    """At RHS 16-64 the tuned kernel stores C one float per lane, so a 4-byte aligned C panel takes
-    it: the launcher accepts it, and both it and Plan::execute give the same bits as with an
-    aligned C, without writing outside the panel."""
+@pytest.mark.parametrize("rhs", [8, 16, 32, 64])
+def test_misaligned_c_stays_on_the_mfma_kernel(rhs):
+    """A C panel 4 bytes past a 16-byte boundary takes the tuned kernel (at RHS 8, rows of 56 and 64
+    store 16 bytes per lane at 4-byte alignment): the launcher accepts it, and both it and
+    Plan::execute give the same bits as with an aligned C, without writing outside the panel."""
     note(f"misaligned C rhs={rhs}")
     c = Case(vb.generate(40, 40, 4, "bimodal8or64", "random", 19), rhs, 19)
     plan = vb.Plan(c.matrix, rhs)

@@ -134,11 +134,9 @@ inline void check_panels(const vbsr_device_view& a, const float* b, const float*
 void launch_scalar(const vbsr_device_view& a, const float* b, float* c, int rhs, hipStream_t stream);
 
 // Row-owned MFMA kernel (row_owned_mfma.hip).  Launch count: 1 (0 for an
-// empty schedule).  Requires row_owned_supported(a, b, c, rhs): B 4-byte
-// aligned (16-byte aligned B takes 16-byte loads), C 16-byte aligned at rhs 8
-// and 4-byte aligned otherwise, and fewer than 2^26 scalar columns (32-bit
-// buffer offsets).
-bool row_owned_supported(const vbsr_device_view& a, const float* b, const float* c, int rhs);
+// empty schedule).  Requires row_owned_supported(a, b, c): float-aligned B
+// and C, and fewer than 2^26 scalar columns (32-bit buffer offsets).
+bool row_owned_supported(const vbsr_device_view& a, const float* b, const float* c);
 void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& schedule, const float* b, float* c,
                       int rhs, hipStream_t stream);
 

@@ -68,6 +68,11 @@ namespace vbsr_amd {
 namespace {
 
 using f32x4 = float __attribute__((ext_vector_type(4)));
+// The same vector at float alignment: B and C panels need only be 4-byte
+// aligned.  gfx950 serves 16-byte global and buffer accesses at any 4-byte
+// aligned address (ROCm runs it in unaligned access mode, and the compiler
+// itself merges adjacent 4-byte accesses into them).
+typedef float f32x4_unaligned __attribute__((ext_vector_type(4), aligned(4)));
 using rsrc_t = __amdgpu_buffer_rsrc_t;
 
 constexpr int kWave = 64;
@@ -180,9 +185,7 @@ struct Launch {
   float* c;
 };
 
-// kAlignedB: B is 16-byte aligned and each lane's four B floats are one
-// 16-byte load; otherwise (B only 4-byte aligned) they are four 4-byte loads.
-template <int RHS, int T, bool kAlignedB>
+template <int RHS, int T>
 __device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, char* lds, int wave, int lane) {
   using Layout = Lds<RHS>;
   constexpr int kRhsTiles = rhs_tiles<RHS>();
@@ -272,14 +275,7 @@ __device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, c
 #pragma unroll
       for (int nt = 0; nt < kRhsTiles; ++nt) {
         const rsrc_t b_rsrc = make_rsrc(b_base + int64_t(nt) * 16 * ldb, b_bytes);
-        if constexpr (kAlignedB) {
-          st.b[nt] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, int(vb), 0, 0));
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            st.b[nt][e] = __builtin_bit_cast(
-                float, __builtin_amdgcn_raw_buffer_load_b32(b_rsrc, int(vb + 4u * uint32_t(e)), 0, 0));
-        }
+        st.b[nt] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, int(vb), 0, 0));
       }
     };
     // Moves A and B through the wave's LDS slots into MFMA layout, then runs
@@ -393,7 +389,8 @@ __device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, c
       for (int v = 0; v < 4; ++v) {
         const int n = 4 * group + v;
         if (n < RHS)
-          *reinterpret_cast<f32x4*>(c_rows + int64_t(n) * ldc) = f32x4{sum[0][v], sum[1][v], sum[2][v], sum[3][v]};
+          *reinterpret_cast<f32x4_unaligned*>(c_rows + int64_t(n) * ldc) =
+              f32x4{sum[0][v], sum[1][v], sum[2][v], sum[3][v]};
       }
     }
     return;
@@ -415,7 +412,7 @@ __device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, c
   }
 }
 
-template <int RHS, bool kAlignedB>
+template <int RHS>
 __global__ __launch_bounds__(kThreads) void row_owned_mfma_kernel(Launch L) {
   __shared__ __attribute__((aligned(16))) char lds[Lds<RHS>::kTotal];
   const int wave = uniform(int(threadIdx.x) / kWave);
@@ -423,30 +420,24 @@ __global__ __launch_bounds__(kThreads) void row_owned_mfma_kernel(Launch L) {
   const RowItem item = L.rows[blockIdx.x];
   if (uniform(item.step_count) < 0) return;  // padding slot: the whole workgroup leaves
   switch ((uniform(item.h) + 15) >> 4) {
-  case 1: row_body<RHS, 1, kAlignedB>(L, item, lds, wave, lane); break;
-  case 2: row_body<RHS, 2, kAlignedB>(L, item, lds, wave, lane); break;
-  case 3: row_body<RHS, 3, kAlignedB>(L, item, lds, wave, lane); break;
-  default: row_body<RHS, 4, kAlignedB>(L, item, lds, wave, lane); break;
+  case 1: row_body<RHS, 1>(L, item, lds, wave, lane); break;
+  case 2: row_body<RHS, 2>(L, item, lds, wave, lane); break;
+  case 3: row_body<RHS, 3>(L, item, lds, wave, lane); break;
+  default: row_body<RHS, 4>(L, item, lds, wave, lane); break;
   }
 }
 
 template <int RHS>
 void launch(const Launch& L, int64_t groups, hipStream_t stream) {
-  if (reinterpret_cast<uintptr_t>(L.b) % 16 == 0)
-    row_owned_mfma_kernel<RHS, true><<<dim3(unsigned(groups)), dim3(kThreads), 0, stream>>>(L);
-  else
-    row_owned_mfma_kernel<RHS, false><<<dim3(unsigned(groups)), dim3(kThreads), 0, stream>>>(L);
+  row_owned_mfma_kernel<RHS><<<dim3(unsigned(groups)), dim3(kThreads), 0, stream>>>(L);
 }
 
 }  // namespace
 
-bool row_owned_supported(const vbsr_device_view& a, const float* b, const float* c, int rhs) {
-  // B loads of 16 bytes, or of 4 bytes for a B that is not 16-byte aligned;
-  // 16-byte C stores at RHS 8 (four-tile rows), 4-byte ones at the other
-  // widths; 32-bit buffer offsets: a B tile spans 15 columns of ld K plus one
-  // step, and must stay below the out-of-range offset.
-  const uintptr_t c_align = rhs == 8 ? 16 : 4;
-  return reinterpret_cast<uintptr_t>(b) % 4 == 0 && reinterpret_cast<uintptr_t>(c) % c_align == 0 &&
+bool row_owned_supported(const vbsr_device_view& a, const float* b, const float* c) {
+  // Float-aligned panels; 32-bit buffer offsets: a B tile spans 15 columns of
+  // ld K plus one step, and must stay below the out-of-range offset.
+  return reinterpret_cast<uintptr_t>(b) % 4 == 0 && reinterpret_cast<uintptr_t>(c) % 4 == 0 &&
          a.scalar_cols < (int64_t(1) << 26);
 }
 
@@ -454,10 +445,8 @@ void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& s, con
                       hipStream_t stream) {
   if (!supported_rhs(rhs)) throw std::invalid_argument("unsupported rhs width");
   check_panels(a, b, c, rhs);
-  if (!row_owned_supported(a, b, c, rhs))
-    throw std::invalid_argument(
-        "row-owned kernel needs a 4-byte aligned B, a 16-byte aligned C at rhs 8 (4-byte at other widths) "
-        "and fewer than 2^26 scalar columns");
+  if (!row_owned_supported(a, b, c))
+    throw std::invalid_argument("row-owned kernel needs fewer than 2^26 scalar columns");
   if (s.groups <= 0) return;
   if (s.groups > int64_t(0x7fffffff)) throw std::invalid_argument("schedule too large for one launch");
   const void* rows = rhs >= 32 && s.rows_wide != nullptr ? s.rows_wide : s.rows;

@@ -8,11 +8,9 @@
 // kernel and the height split has no counterpart.  The matrix's row schedule
 // (schedule.cpp) orders and places the rows instead.
 //
-// A C panel that is not 16-byte aligned at RHS 8 (the kernel's vector
-// stores there need it), and matrices with 2^26 or more scalar columns (its
-// 32-bit buffer offsets), go to the order-preserving kernel, which has
-// neither limit.  A B panel that is not 16-byte aligned stays on the MFMA
-// kernel, which then loads B 4 bytes at a time.
+// Matrices with 2^26 or more scalar columns (the MFMA kernel's 32-bit
+// buffer offsets) go to the order-preserving kernel, which has no such
+// limit.  Any float-aligned B and C panels stay on the MFMA kernel.
 #include "internal.hpp"
 
 namespace vbsr_amd {
@@ -27,7 +25,7 @@ Plan::Plan(const DeviceMatrix& matrix, const vbsr_plan_options& o)
 }
 
 void Plan::execute(const float* b, float* c, hipStream_t stream) const {
-  if (row_owned_supported(a, b, c, options.rhs_width))
+  if (row_owned_supported(a, b, c))
     launch_row_owned(a, schedule, b, c, options.rhs_width, stream);
   else
     launch_scalar(a, b, c, options.rhs_width, stream);
