@@ -7,9 +7,13 @@
 // are bit-identical to the reference's.  It is the GPU-side order oracle and
 // the profiling baseline, not the fast path.
 //
-// Mapping: one workgroup (256 lanes = 4 waves) per block row; lanes stride
-// over the row's h x rhs outputs with the local row fastest, so a wave's A
-// loads for one k are consecutive floats of one block column.
+// Mapping: one workgroup per block row.  Lane (r, g) owns local row r and
+// the adjacent output columns of group g: 4 groups of RHS/4 columns (256
+// lanes), or 8 groups of 8 at RHS 64 (512 lanes), so gh lanes cover the row
+// in one pass and each A value a lane loads feeds RHS/groups fmaf chains.
+// Each block's B slice (w x RHS floats) is staged once per workgroup in LDS,
+// double-buffered with one barrier per block, stored k-major with a padded
+// row (RHS + 4 floats) so a lane's columns are one 8- to 64-byte read.
 #include <hip/hip_runtime.h>
 
 #include "../internal.hpp"
@@ -17,36 +21,87 @@
 namespace vbsr_amd {
 namespace {
 
-constexpr int kScalarThreads = 256;
+constexpr int kMaxBlockDim = 64;  // largest block height and width
+
+// Column groups per local row, and the workgroup that covers 64 rows of them.
+template <int RHS>
+constexpr int scalar_groups() {
+  return RHS == 64 ? 8 : 4;
+}
+template <int RHS>
+constexpr int scalar_threads() {
+  return scalar_groups<RHS>() * kMaxBlockDim;
+}
 
 template <int RHS>
-__global__ __launch_bounds__(kScalarThreads) void row_owned_scalar_kernel(vbsr_device_view a,
+__global__ __launch_bounds__(scalar_threads<RHS>()) void row_owned_scalar_kernel(vbsr_device_view a,
                                                                           const float* __restrict__ b,
                                                                           float* __restrict__ c) {
+  constexpr int kGroups = scalar_groups<RHS>();
+  constexpr int kThreads = scalar_threads<RHS>();
+  constexpr int kCols = RHS / kGroups;  // output columns per lane
+  constexpr int kLd = RHS + 4;          // LDS row of one k of a B slice
+  __shared__ __attribute__((aligned(16))) float slice[2][kMaxBlockDim * kLd];
+
   const int row = blockIdx.x;
+  const int tid = int(threadIdx.x);
   const int h = a.row_size[row];
   const int first = a.row_ptr[row];
   const int last = a.row_ptr[row + 1];
-  const int64_t out_base = a.row_scalar_off[row];
+  const int r = tid % h;
+  const int g = tid / h;
+  const bool owner = g < kGroups;  // kGroups * h lanes own outputs; the rest only stage B
 
-  for (int item = threadIdx.x; item < h * RHS; item += kScalarThreads) {
-    const int r = item % h;
-    const int n = item / h;
-    float acc = 0.0f;
-    for (int blk = first; blk < last; ++blk) {
-      const int col = a.block_col[blk];
-      const int w = a.col_size[col];
+  // Stages block blk's B slice: B[col0 + k, n] for k < w, n < RHS at k * kLd + n.
+  auto stage = [&](int blk, float* dst) {
+    const int col = a.block_col[blk];
+    const int w = a.col_size[col];
+    const float* src = b + a.col_scalar_off[col];
+    const int k = tid % kMaxBlockDim;
+    if (k < w)
+      for (int n = tid / kMaxBlockDim; n < RHS; n += kThreads / kMaxBlockDim)
+        dst[k * kLd + n] = src[k + int64_t(n) * a.scalar_cols];
+  };
+
+  float acc[kCols];
+#pragma unroll
+  for (int j = 0; j < kCols; ++j) acc[j] = 0.0f;
+
+  if (first < last) stage(first, slice[0]);
+  __syncthreads();
+  for (int blk = first; blk < last; ++blk) {
+    const int buf = (blk - first) & 1;
+    if (blk + 1 < last) stage(blk + 1, slice[buf ^ 1]);
+    if (owner) {
+      const int w = a.col_size[a.block_col[blk]];
       const float* a_col = a.values + a.value_off[blk] + r;
-      const float* b_col = b + a.col_scalar_off[col] + int64_t(n) * a.scalar_cols;
-      for (int k = 0; k < w; ++k) acc = __builtin_fmaf(a_col[int64_t(k) * h], b_col[k], acc);
+      const float* bs = slice[buf] + g * kCols;
+      // w is a multiple of 8: eight A loads in flight, then their fmafs in
+      // k order.
+      for (int k0 = 0; k0 < w; k0 += 8) {
+        float av[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) av[i] = a_col[int64_t(k0 + i) * h];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float* bk = bs + (k0 + i) * kLd;
+#pragma unroll
+          for (int j = 0; j < kCols; ++j) acc[j] = __builtin_fmaf(av[i], bk[j], acc[j]);
+        }
+      }
     }
-    c[out_base + r + int64_t(n) * a.scalar_rows] = acc;
+    __syncthreads();
+  }
+  if (owner) {
+    float* c_row = c + a.row_scalar_off[row] + r;
+#pragma unroll
+    for (int j = 0; j < kCols; ++j) c_row[int64_t(g * kCols + j) * a.scalar_rows] = acc[j];
   }
 }
 
 template <int RHS>
 void launch(const vbsr_device_view& a, const float* b, float* c, hipStream_t stream) {
-  row_owned_scalar_kernel<RHS><<<dim3(unsigned(a.block_rows)), dim3(kScalarThreads), 0, stream>>>(a, b, c);
+  row_owned_scalar_kernel<RHS><<<dim3(unsigned(a.block_rows)), dim3(scalar_threads<RHS>()), 0, stream>>>(a, b, c);
 }
 
 }  // namespace
