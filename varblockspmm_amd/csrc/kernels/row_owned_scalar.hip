@@ -26,7 +26,7 @@ constexpr int kMaxBlockDim = 64;  // largest block height and width
 // Column groups per local row, and the workgroup that covers 64 rows of them.
 template <int RHS>
 constexpr int scalar_groups() {
-  return RHS == 64 ? 8 : 4;
+  return RHS >= 32 ? 8 : 4;
 }
 template <int RHS>
 constexpr int scalar_threads() {
