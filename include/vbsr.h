@@ -163,8 +163,10 @@ int vbsr_plan_launch_count(const vbsr_plan* plan);
 /* launch_row_owned (vbsr.hpp:158-159; row_owned.cu:397-423): the tuned
  * row-owned kernel for `rhs` over `matrix`, scheduled by `schedule` (from
  * vbsr_matrix_row_schedule of the matrix that `matrix` views; the reference
- * passes row_shape_order/small/large in the same role).  K must be below
- * 2^26 (VBSR_INVALID_ARGUMENT otherwise; vbsr_plan_execute takes any K). */
+ * passes row_shape_order/small/large in the same role).  K must be at most
+ * 153,391,684 at rhs 8 and 71,582,785 otherwise, so that B offsets within a
+ * 16-column tile fit 32 bits (VBSR_INVALID_ARGUMENT otherwise;
+ * vbsr_plan_execute takes any K). */
 int vbsr_launch_row_owned(const vbsr_device_view* matrix, const vbsr_row_schedule* schedule,
                           const float* B, float* C, int32_t rhs, hipStream_t stream);
 

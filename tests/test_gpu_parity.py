@@ -525,7 +525,7 @@ def test_grouped_gemm_plan_config3_and_empty_rows():
 def largest_offset_case(scalar_cols, rhs):
     """Three block rows over scalar_cols / 64 block columns of width 64, using the first, a middle
     and the last block column, and a B panel (ld = scalar_cols) that is zero except where those
-    columns are read.  The panel is scalar_cols * rhs floats (2-4 GiB); np.zeros leaves its
+    columns are read.  The panel is scalar_cols * rhs floats (4.6-4.9 GB); np.zeros leaves its
     untouched pages unallocated on the host."""
     ncols = scalar_cols // 64
     host = hand_made([16, 40, 8], [64] * ncols, [[0, ncols - 1], [ncols // 2], [ncols - 1]], seed=5)
@@ -549,10 +549,11 @@ def check_against_oracle(host, b, rhs, result, name):
     assert normwise <= NORMWISE_TOL and rel_l2 <= REL_L2_TOL and elementwise <= ELEMENTWISE_TOL, name
 
 
-def test_largest_b_offsets_take_the_mfma_kernel():
-    """K = 2^26 - 64, the largest K the MFMA kernel takes: its 32-bit B offsets reach
-    15 * K * 4 + 64 bytes, just under 2^32."""
-    scalar_cols, rhs = (1 << 26) - 64, 16
+@pytest.mark.parametrize("scalar_cols,rhs", [(71_582_784, 16), (153_391_680, 8)])
+def test_largest_b_offsets_take_the_mfma_kernel(scalar_cols, rhs):
+    """The largest K (in whole 64-wide block columns) the MFMA kernel takes: its 32-bit B offsets
+    within a 16-column tile reach (min(rhs, 16) - 1) * K * 4 + 64 bytes, 64 bytes or more below
+    the out-of-range offset 0xfffffff0."""
     note(f"largest offsets: K={scalar_cols} rhs={rhs} (B {scalar_cols * rhs * 4 / 2**30:.1f} GiB)")
     host, b = largest_offset_case(scalar_cols, rhs)
     matrix = vb.Matrix(host)
@@ -579,8 +580,9 @@ def test_largest_b_offsets_take_the_mfma_kernel():
 
 
 def test_k_at_the_offset_limit_goes_to_the_order_preserving_kernel():
-    """K = 2^26: the MFMA launcher refuses it and the plan runs the order-preserving kernel."""
-    scalar_cols, rhs = 1 << 26, 8
+    """One block column past the largest K at RHS 16: the MFMA launcher refuses it and the plan runs
+    the order-preserving kernel."""
+    scalar_cols, rhs = 71_582_848, 16
     note(f"offset limit: K={scalar_cols} rhs={rhs}")
     host, b = largest_offset_case(scalar_cols, rhs)
     matrix = vb.Matrix(host)

@@ -134,9 +134,10 @@ inline void check_panels(const vbsr_device_view& a, const float* b, const float*
 void launch_scalar(const vbsr_device_view& a, const float* b, float* c, int rhs, hipStream_t stream);
 
 // Row-owned MFMA kernel (row_owned_mfma.hip).  Launch count: 1 (0 for an
-// empty schedule).  Requires row_owned_supported(a, b, c): float-aligned B
-// and C, and fewer than 2^26 scalar columns (32-bit buffer offsets).
-bool row_owned_supported(const vbsr_device_view& a, const float* b, const float* c);
+// empty schedule).  Requires row_owned_supported(a, b, c, rhs): float-aligned
+// B and C, and K small enough for 32-bit B offsets within a 16-column tile
+// (K <= 153,391,684 at rhs 8, 71,582,785 otherwise).
+bool row_owned_supported(const vbsr_device_view& a, const float* b, const float* c, int rhs);
 void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& schedule, const float* b, float* c,
                       int rhs, hipStream_t stream);
 

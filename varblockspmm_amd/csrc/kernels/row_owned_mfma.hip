@@ -434,19 +434,23 @@ void launch(const Launch& L, int64_t groups, hipStream_t stream) {
 
 }  // namespace
 
-bool row_owned_supported(const vbsr_device_view& a, const float* b, const float* c) {
-  // Float-aligned panels; 32-bit buffer offsets: a B tile spans 15 columns of
-  // ld K plus one step, and must stay below the out-of-range offset.
+bool row_owned_supported(const vbsr_device_view& a, const float* b, const float* c, int rhs) {
+  // Float-aligned panels; 32-bit buffer offsets: a B tile's resource spans
+  // min(rhs, 16) - 1 columns of ld K plus one step, and must end at least
+  // 64 bytes below the out-of-range offset (K <= 153,391,684 at RHS 8,
+  // 71,582,785 otherwise).
+  const uint64_t span = uint64_t(rhs < 16 ? rhs - 1 : 15) * uint64_t(a.scalar_cols) * 4u + 64u;
   return reinterpret_cast<uintptr_t>(b) % 4 == 0 && reinterpret_cast<uintptr_t>(c) % 4 == 0 &&
-         a.scalar_cols < (int64_t(1) << 26);
+         span + 64u <= kOutOfRange;
 }
 
 void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& s, const float* b, float* c, int rhs,
                       hipStream_t stream) {
   if (!supported_rhs(rhs)) throw std::invalid_argument("unsupported rhs width");
   check_panels(a, b, c, rhs);
-  if (!row_owned_supported(a, b, c))
-    throw std::invalid_argument("row-owned kernel needs fewer than 2^26 scalar columns");
+  if (!row_owned_supported(a, b, c, rhs))
+    throw std::invalid_argument(
+        "row-owned kernel needs (min(rhs, 16) - 1) * K * 4 + 128 <= 0xfffffff0 (its 32-bit B offsets)");
   if (s.groups <= 0) return;
   if (s.groups > int64_t(0x7fffffff)) throw std::invalid_argument("schedule too large for one launch");
   const void* rows = rhs >= 32 && s.rows_wide != nullptr ? s.rows_wide : s.rows;

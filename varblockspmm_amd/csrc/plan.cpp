@@ -8,9 +8,9 @@
 // kernel and the height split has no counterpart.  The matrix's row schedule
 // (schedule.cpp) orders and places the rows instead.
 //
-// Matrices with 2^26 or more scalar columns (the MFMA kernel's 32-bit
-// buffer offsets) go to the order-preserving kernel, which has no such
-// limit.  Any float-aligned B and C panels stay on the MFMA kernel.
+// Matrices with more scalar columns than the MFMA kernel's 32-bit B offsets
+// reach (K > 153,391,684 at RHS 8, K > 71,582,785 otherwise) go to the
+// order-preserving kernel, which has no such limit.  Any float-aligned B and C panels stay on the MFMA kernel.
 #include "internal.hpp"
 
 namespace vbsr_amd {
@@ -25,7 +25,7 @@ Plan::Plan(const DeviceMatrix& matrix, const vbsr_plan_options& o)
 }
 
 void Plan::execute(const float* b, float* c, hipStream_t stream) const {
-  if (row_owned_supported(a, b, c))
+  if (row_owned_supported(a, b, c, options.rhs_width))
     launch_row_owned(a, schedule, b, c, options.rhs_width, stream);
   else
     launch_scalar(a, b, c, options.rhs_width, stream);
