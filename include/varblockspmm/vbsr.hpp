@@ -4,8 +4,8 @@
 // header-only over the C ABI in <vbsr.h>.  Streams are hipStream_t.
 //
 // Differences from the reference header:
-//  - cpu_reference is not part of the library.  It is the test oracle and
-//    lives in oracle/vbsr_oracle.h (orc_cpu_reference).
+//  - cpu_reference validates the matrix before reading it (the reference
+//    reads an invalid one out of bounds).
 //  - ScalarCsrPlan runs on rocSPARSE instead of cuSPARSE, and GroupedGemmPlan
 //    on rocBLAS (one batched GEMM per slot and block shape) instead of
 //    cuBLAS grouped GEMM.  The one-shot baseline helpers are not provided.
@@ -158,6 +158,20 @@ inline HostMatrix generate(const GeneratorOptions& o) {
   m.value_off.assign(v.value_off, v.value_off + v.value_off_len);
   m.values.assign(v.values, v.values + v.values_len);
   return m;
+}
+
+/** Computes `C = A * B` on the CPU with double-precision accumulation
+ * (reference vbsr.hpp:82-87): the reference's arithmetic, so the result is
+ * bit-identical to the reference's.  `B` and the returned `C` are
+ * column-major; `B` must hold `matrix.scalar_cols() * rhs` elements
+ * (std::invalid_argument "B size" otherwise).  The matrix is validated first. */
+inline std::vector<float> cpu_reference(const HostMatrix& matrix, const std::vector<float>& B, int rhs) {
+  const vbsr_host_view v = matrix.view();
+  std::vector<float> C;
+  int64_t c_len = 0;
+  if (rhs > 0 && !__builtin_mul_overflow(matrix.scalar_rows(), int64_t(rhs), &c_len) && c_len > 0) C.resize(size_t(c_len));
+  detail::check(vbsr_cpu_reference(&v, B.data(), int64_t(B.size()), rhs, C.data(), int64_t(C.size())));
+  return C;
 }
 
 /** Kernel selection; SplitRow is reserved and rejected (reference vbsr.hpp:91). */

@@ -122,6 +122,19 @@ void vbsr_host_matrix_destroy(vbsr_host_matrix* matrix);
  * into out[0..count). */
 int vbsr_make_random_input(int64_t count, uint64_t seed, float* out);
 
+/* cpu_reference (vbsr.hpp:82-87; vbsr.cpp:167-201): C = A * B on the host,
+ * single-threaded, each block's contribution to C[r, n] summed in double over
+ * k ascending and added to C in float, blocks in row_ptr order -- the
+ * reference's arithmetic, so its results are bit-identical to the
+ * reference's.  B holds b_len == scalar_cols * rhs floats and C receives
+ * c_len == scalar_rows * rhs floats (column-major, fully overwritten); a
+ * wrong size is VBSR_INVALID_ARGUMENT ("B size", as the reference's
+ * std::invalid_argument).  Unlike the reference, the matrix is validated
+ * first and negative scalar offset starts are rejected, so no invalid view
+ * is read out of bounds.  Host memory only; no GPU is used. */
+int vbsr_cpu_reference(const vbsr_host_view* host, const float* B, int64_t b_len, int32_t rhs, float* C,
+                       int64_t c_len);
+
 /* Matrix(const HostMatrix&) (vbsr.hpp:44; vbsr.cpp:84-113): validates, then
  * copies every array to the current HIP device and builds the row schedule.
  * Additionally rejects (VBSR_INVALID_ARGUMENT) row/col scalar offsets that do
@@ -141,7 +154,7 @@ int64_t vbsr_matrix_scalar_cols(const vbsr_matrix* matrix);
  * arrays owned by the matrix; opaque to callers. */
 typedef struct vbsr_row_schedule {
   const void* steps;     /* device: one 16-byte record per k step */
-  const void* rows;      /* device: one 32-byte row item per workgroup, launch order for rhs 8 and 16 */
+  const void* rows;      /* device: one 96-byte row item per workgroup, launch order for rhs 8 and 16 */
   int64_t groups;        /* workgroups of one launch */
   int32_t step_limit;    /* index of the last step record */
   const void* rows_wide; /* device: the same row items, launch order for rhs 32 and 64 */

@@ -133,6 +133,17 @@ void run_case(vbsr::Distribution distribution, int degree, int rhs, bool local, 
   orc_fmaf_order(&ov, input.data(), int64_t(input.size()), rhs, emulated.data());
   orc_abs_product_sum(&ov, input.data(), int64_t(input.size()), rhs, bound.data());
 
+  // The library's own cpu_reference, called as test_main.cpp:73 calls it:
+  // the reference's arithmetic, so bit-identical to the oracle's.
+  const std::vector<float> library_reference = vbsr::cpu_reference(host, input, rhs);
+  if (library_reference.size() != reference.size() ||
+      std::memcmp(library_reference.data(), reference.data(), reference.size() * sizeof(float)) != 0)
+    throw std::runtime_error("vbsr::cpu_reference differs from the oracle (degree " + std::to_string(degree) +
+                             ", rhs " + std::to_string(rhs) + ", seed " + std::to_string(seed) + ")");
+  std::vector<float> short_input(input.begin(), input.end() - 1);
+  expect_invalid_argument([&] { (void)vbsr::cpu_reference(host, short_input, rhs); },
+                          "cpu_reference accepted a B of the wrong size");
+
   vbsr::Matrix device(host);
   DeviceBuffer b(input.size()), c(reference.size());
   hip_ok(hipMemcpy(b.ptr, input.data(), input.size() * sizeof(float), hipMemcpyHostToDevice), "upload B");

@@ -11,6 +11,7 @@ import pytest
 
 import oracle_ffi as o
 import varblockspmm_amd as vb
+from reference_cases import reference_cases
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -233,3 +234,80 @@ def test_grouped_gemm_plan_rejects_bad_input_before_touching_the_gpu():
     assert lib.vbsr_gemm_plan_execute(None, None, None, None) == vb.VBSR_INVALID_ARGUMENT
     assert lib.vbsr_gemm_plan_launch_count(None) == 0
     lib.vbsr_gemm_plan_destroy(None)
+
+
+# ---- cpu_reference (vbsr.hpp:82-87; vbsr.cpp:167-201), exported by the library ----------------------------
+
+
+@pytest.mark.parametrize("case", reference_cases(), ids=lambda c: "{}-d{}-n{}-{}-s{}".format(*c))
+def test_cpu_reference_is_bit_identical_to_the_oracle(case):
+    """The library's cpu_reference against the oracle's restatement of the reference's, bit for bit, on the
+    reference test's own parameter matrix (tests/test_main.cpp:145-161, the cases it calls cpu_reference on
+    at :73)."""
+    distribution, degree, rhs, locality, seed = case
+    host = vb.generate(9, 17, degree, distribution, locality, seed)
+    b = vb.make_random_input(host.scalar_cols * rhs, seed)
+    np.testing.assert_array_equal(vb.cpu_reference(host, b, rhs), o.cpu_reference(as_oracle(host), b, rhs))
+
+
+def test_cpu_reference_is_bit_identical_to_the_oracle_at_configuration_1():
+    """BASELINE configuration 1, the CPU-only one: 1024 block rows, degree 4, high sizes, clamped local
+    columns, RHS 8, seed 1."""
+    host = vb.generate(1024, 1024, 4, "high", "clamped", 1)
+    b = vb.make_random_input(host.scalar_cols * 8, 1)
+    np.testing.assert_array_equal(vb.cpu_reference(host, b, 8), o.cpu_reference(as_oracle(host), b, 8))
+
+
+def test_cpu_reference_accepts_any_rhs_and_shifted_row_offsets():
+    """Like the reference's, it takes any non-negative RHS width (not only the kernels' four), and row offsets
+    that start above 0 (those C rows stay zero)."""
+    host = vb.generate(6, 7, 2, "bimodal", "random", 5)
+    for rhs in (1, 3, 12):
+        b = vb.make_random_input(host.scalar_cols * rhs, rhs)
+        np.testing.assert_array_equal(vb.cpu_reference(host, b, rhs), o.cpu_reference(as_oracle(host), b, rhs))
+    assert len(vb.cpu_reference(host, np.zeros(0, np.float32), 0)) == 0
+    shifted = host.copy()
+    shifted.row_scalar_off = shifted.row_scalar_off + 16
+    b = vb.make_random_input(host.scalar_cols * 8, 2)
+    c = vb.cpu_reference(shifted, b, 8).reshape(8, -1)
+    assert np.all(c[:, :16] == 0)
+    np.testing.assert_array_equal(c[:, 16:], vb.cpu_reference(host, b, 8).reshape(8, -1))
+
+
+def test_cpu_reference_rejects_what_the_reference_rejects_and_invalid_matrices():
+    host = vb.generate(4, 6, 2, "high", "random", 5)
+    b = vb.make_random_input(host.scalar_cols * 8, 1)
+    for bad_b in (b[:-1], np.concatenate([b, b[:1]])):
+        with pytest.raises(ValueError, match="B size"):  # vbsr.cpp:169-171
+            vb.cpu_reference(host, bad_b, 8)
+    with pytest.raises(ValueError, match="B size"):
+        vb.cpu_reference(host, b, -8)
+    bad = host.copy()
+    bad.row_size[0] = 7
+    with pytest.raises(ValueError):
+        vb.cpu_reference(bad, b, 8)
+    negative = host.copy()
+    negative.col_scalar_off = negative.col_scalar_off - 8
+    with pytest.raises(ValueError, match="negative"):
+        vb.cpu_reference(negative, b, 8)
+    lib = vb.library()
+    assert lib.vbsr_cpu_reference(None, None, 0, 8, None, 0) == vb.VBSR_INVALID_ARGUMENT
+
+
+def test_cpu_reference_holds_the_closed_forms():
+    """Identity blocks copy B's slices; a unit B column extracts A's columns (independent of the oracle)."""
+    host = vb.generate(5, 5, 1, "high", "random", 9)
+    h = host.row_size
+    w = host.col_size[host.block_col]
+    host.values = np.concatenate([np.eye(hh, ww, dtype=np.float32).ravel(order="F") for hh, ww in zip(h, w)])
+    host.value_off = np.concatenate([[0], np.cumsum(h * w)]).astype(np.int64)
+    host.validate()
+    rhs = 8
+    b = vb.make_random_input(host.scalar_cols * rhs, 4)
+    c = vb.cpu_reference(host, b, rhs).reshape(rhs, -1)
+    bb = b.reshape(rhs, -1)
+    for i in range(host.block_rows):
+        r0, c0 = host.row_scalar_off[i], host.col_scalar_off[host.block_col[i]]
+        m = min(h[i], w[i])
+        np.testing.assert_array_equal(c[:, r0:r0 + m], bb[:, c0:c0 + m])
+        assert np.all(c[:, r0 + m:r0 + h[i]] == 0)

@@ -71,6 +71,8 @@ SIGNATURES = {
     "vbsr_host_matrix_view": (ctypes.c_int, [_P, ctypes.POINTER(HostView)]),
     "vbsr_host_matrix_destroy": (None, [_P]),
     "vbsr_make_random_input": (ctypes.c_int, [ctypes.c_int64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_float)]),
+    "vbsr_cpu_reference": (ctypes.c_int, [ctypes.POINTER(HostView), ctypes.POINTER(ctypes.c_float), ctypes.c_int64,
+                                          ctypes.c_int32, ctypes.POINTER(ctypes.c_float), ctypes.c_int64]),
     "vbsr_matrix_create": (ctypes.c_int, [ctypes.POINTER(HostView), ctypes.POINTER(_P)]),
     "vbsr_matrix_destroy": (None, [_P]),
     "vbsr_matrix_device_view": (ctypes.c_int, [_P, ctypes.POINTER(DeviceView)]),
@@ -229,6 +231,20 @@ def make_random_input(count, seed):
     out = np.empty(int(count), dtype=np.float32)
     _check(library().vbsr_make_random_input(int(count), int(seed), out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
     return out
+
+
+def cpu_reference(matrix, B, rhs_width):
+    """cpu_reference (vbsr.hpp:82-87; vbsr.cpp:167-201): C = A*B on the host in the reference's arithmetic
+    (double sum per block, FP32 across blocks).  B and the returned C are column-major float32 numpy arrays;
+    raises ValueError ("B size") when B does not hold scalar_cols * rhs_width floats."""
+    b = np.ascontiguousarray(B, dtype=np.float32)
+    rhs = int(rhs_width)
+    c = np.empty(max(0, matrix.scalar_rows * rhs), dtype=np.float32)
+    view = matrix._view()
+    fp = ctypes.POINTER(ctypes.c_float)
+    _check(library().vbsr_cpu_reference(ctypes.byref(view), b.ctypes.data_as(fp), len(b), rhs, c.ctypes.data_as(fp),
+                                        len(c)))
+    return c
 
 
 class Matrix:

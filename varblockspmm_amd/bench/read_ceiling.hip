@@ -1,0 +1,152 @@
+// read_ceiling: the read bandwidth an MI355X delivers to a streaming kernel,
+// from each level a kernel's L2 misses can be served by.  The row-owned
+// kernel's traffic (its L2 misses, counted by FETCH_SIZE) is compared with
+// these rates to say what bounds it.
+//
+// Cases (one JSON line each, median of --reps timed launches):
+//   dram      1 GiB read once per launch; a second 1 GiB buffer is read
+//             between launches, so nothing of the first is cached in L2 or
+//             in the 256 MB Infinity Cache (MALL).
+//   mall      96 MiB read once per launch, after a warm-up launch: each XCD
+//             streams its eighth (12 MiB, three times its 4 MiB L2) in order,
+//             so every access misses L2 and the Infinity Cache serves it.
+//   l2        16 MiB read 8 times per launch: each XCD's eighth (2 MiB) stays
+//             in its L2.
+// Each case runs with plain and with non-temporal 16-byte loads.
+//
+// Workgroup i runs on XCD i mod 8; the grid is a multiple of 8 and each
+// workgroup reads 16 KiB chunks i, i + grid, ..., so each XCD reads one
+// eighth of the buffer.
+//
+//   make -C varblockspmm_amd/bench read_ceiling && varblockspmm_amd/bench/read_ceiling
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+namespace {
+
+using f32x4 = float __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;  // 16-byte loads in flight per lane
+
+void check(hipError_t status, const char* what) {
+  if (status != hipSuccess) {
+    std::fprintf(stderr, "%s: %s\n", what, hipGetErrorString(status));
+    std::exit(1);
+  }
+}
+
+template <bool kNonTemporal>
+__global__ __launch_bounds__(kThreads) void read_kernel(const f32x4* __restrict__ data, int64_t count, int passes,
+                                                        float* __restrict__ sink) {
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int64_t chunk = int64_t(kThreads) * kUnroll;
+  const int64_t stride = int64_t(gridDim.x) * chunk;
+  for (int pass = 0; pass < passes; ++pass) {
+    for (int64_t base = int64_t(blockIdx.x) * chunk + threadIdx.x; base < count; base += stride) {
+      f32x4 v[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t i = base + int64_t(u) * kThreads;
+        if (i < count)
+          v[u] = kNonTemporal ? __builtin_nontemporal_load(data + i) : data[i];
+        else
+          v[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) acc += v[u];
+    }
+  }
+  // Keeps the loads live; the buffers hold zeros, so nothing is written.
+  const float total = acc.x + acc.y + acc.z + acc.w;
+  if (total != 0.0f) sink[blockIdx.x * kThreads + threadIdx.x] = total;
+}
+
+struct Result {
+  double median_us, gbps;
+};
+
+template <bool kNonTemporal>
+Result run(const float* buffer, int64_t bytes, int passes, const float* flush, int64_t flush_bytes, int reps,
+           int grid, float* sink, hipStream_t stream) {
+  const int64_t count = bytes / 16;
+  const auto launch = [&](const float* p, int64_t n, int k) {
+    read_kernel<kNonTemporal><<<grid, kThreads, 0, stream>>>(reinterpret_cast<const f32x4*>(p), n, k, sink);
+  };
+  hipEvent_t start, stop;
+  check(hipEventCreateWithFlags(&start, hipEventDisableSystemFence), "hipEventCreate");
+  check(hipEventCreateWithFlags(&stop, hipEventDisableSystemFence), "hipEventCreate");
+  launch(buffer, count, passes);  // warm-up (and, for mall/l2, fills the caches)
+  check(hipStreamSynchronize(stream), "warm-up");
+  std::vector<double> us;
+  for (int r = 0; r < reps; ++r) {
+    if (flush != nullptr) launch(flush, flush_bytes / 16, 1);
+    check(hipEventRecord(start, stream), "record");
+    launch(buffer, count, passes);
+    check(hipEventRecord(stop, stream), "record");
+    check(hipEventSynchronize(stop), "sync");
+    float ms = 0;
+    check(hipEventElapsedTime(&ms, start, stop), "elapsed");
+    us.push_back(double(ms) * 1000.0);
+  }
+  check(hipGetLastError(), "launch");
+  std::sort(us.begin(), us.end());
+  const double median = us[us.size() / 2];
+  check(hipEventDestroy(start), "destroy");
+  check(hipEventDestroy(stop), "destroy");
+  return {median, double(bytes) * passes / (median * 1e3)};
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  int reps = 20;
+  for (int i = 1; i < argc; ++i)
+    if (std::strcmp(argv[i], "--reps") == 0 && i + 1 < argc) reps = std::max(1, std::atoi(argv[++i]));
+
+  hipDeviceProp_t props;
+  check(hipGetDeviceProperties(&props, 0), "hipGetDeviceProperties");
+  const int grid = props.multiProcessorCount * 8;  // 8 workgroups per CU, a multiple of the 8 XCDs
+
+  const int64_t GiB = int64_t(1) << 30, MiB = int64_t(1) << 20;
+  float *dram = nullptr, *flush = nullptr, *sink = nullptr;
+  check(hipMalloc(&dram, size_t(GiB)), "hipMalloc");
+  check(hipMalloc(&flush, size_t(GiB)), "hipMalloc");
+  check(hipMalloc(&sink, size_t(grid) * kThreads * sizeof(float)), "hipMalloc");
+  check(hipMemset(dram, 0, size_t(GiB)), "hipMemset");
+  check(hipMemset(flush, 0, size_t(GiB)), "hipMemset");
+  hipStream_t stream;
+  check(hipStreamCreate(&stream), "hipStreamCreate");
+
+  struct Case {
+    const char* name;
+    int64_t bytes;
+    int passes;
+    bool flushed;
+  };
+  const Case cases[] = {{"dram", GiB, 1, true}, {"mall", 96 * MiB, 1, false}, {"l2", 16 * MiB, 8, false}};
+  for (const Case& c : cases) {
+    for (const bool nt : {false, true}) {
+      const Result r = nt ? run<true>(dram, c.bytes, c.passes, c.flushed ? flush : nullptr, GiB, reps, grid, sink,
+                                      stream)
+                          : run<false>(dram, c.bytes, c.passes, c.flushed ? flush : nullptr, GiB, reps, grid, sink,
+                                       stream);
+      std::printf("{\"case\": \"%s\", \"loads\": \"%s\", \"bytes_per_pass\": %lld, \"passes\": %d, \"median_us\": "
+                  "%.2f, \"GB_per_s\": %.1f, \"grid\": %d, \"reps\": %d}\n",
+                  c.name, nt ? "nontemporal" : "plain", static_cast<long long>(c.bytes), c.passes, r.median_us,
+                  r.gbps, grid, reps);
+      std::fflush(stdout);
+    }
+  }
+  check(hipStreamDestroy(stream), "hipStreamDestroy");
+  check(hipFree(dram), "hipFree");
+  check(hipFree(flush), "hipFree");
+  check(hipFree(sink), "hipFree");
+  return 0;
+}

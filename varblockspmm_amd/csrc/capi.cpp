@@ -97,6 +97,14 @@ int vbsr_make_random_input(int64_t count, uint64_t seed, float* out) {
   });
 }
 
+int vbsr_cpu_reference(const vbsr_host_view* host, const float* B, int64_t b_len, int32_t rhs, float* C,
+                       int64_t c_len) {
+  return guarded([&] {
+    require(host, "host");
+    vbsr_amd::cpu_reference(*host, B, b_len, rhs, C, c_len);
+  });
+}
+
 int vbsr_matrix_create(const vbsr_host_view* host, vbsr_matrix** out) {
   return guarded([&] {
     require(host, "host");

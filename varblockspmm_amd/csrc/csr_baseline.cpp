@@ -113,7 +113,7 @@ void CsrPlan::release() noexcept {
 CsrPlan::~CsrPlan() { release(); }
 
 void CsrPlan::execute(const float* b, float* c, hipStream_t stream) {
-  if (b == nullptr || c == nullptr) throw std::invalid_argument("B and C must be device pointers");
+  check_panels(rows_, cols_, b, c, rhs_);
   check_rocsparse(rocsparse_set_stream(handle_, stream), "rocsparse_set_stream");
   const float one = 1.0f, zero = 0.0f;
   auto spmm = [&](rocsparse_spmm_stage stage, size_t* bytes, void* buffer) {

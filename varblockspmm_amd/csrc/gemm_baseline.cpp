@@ -122,7 +122,7 @@ void GemmPlan::release() noexcept {
 GemmPlan::~GemmPlan() { release(); }
 
 void GemmPlan::execute(const float* b, float* c, hipStream_t stream) {
-  if (b == nullptr || c == nullptr) throw std::invalid_argument("B and C must be device pointers");
+  check_panels(rows_, cols_, b, c, rhs_);
   check_rocblas(rocblas_set_stream(handle_, stream), "rocblas_set_stream");
   check_hip(hipMemsetAsync(c, 0, size_t(rows_) * size_t(rhs_) * sizeof(float), stream), "hipMemsetAsync");
   fill_batch_pointers(b_offset_, c_offset_, entries_, b, c, b_pointers_, c_pointers_, stream);

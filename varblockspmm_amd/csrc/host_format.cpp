@@ -165,6 +165,12 @@ HostMatrix generate(const vbsr_generator_options& o) {
   m.row_ptr.push_back(0);
   m.value_off.push_back(0);
 
+  // Reserve about the expected value count (each row's height times degree
+  // times the mean block width) so that the packed values grow in one piece.
+  const double mean_width = double(m.col_scalar_off.back()) / double(o.block_cols);
+  const double expected = double(m.row_scalar_off.back()) * double(o.degree) * mean_width;
+  m.values.reserve(size_t(expected * 1.05) + 65536);
+
   std::uniform_real_distribution<float> value(-1.0f, 1.0f);
   const uint64_t window = uint64_t(2 * o.degree + 1);
   std::vector<int32_t> chosen;

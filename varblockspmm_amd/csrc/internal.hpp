@@ -35,6 +35,11 @@ HostMatrix generate(const vbsr_generator_options& options);
 // make_random_input (tests/test_main.cpp:42-51).
 void make_random_input(int64_t count, uint64_t seed, float* out);
 
+// cpu_reference (vbsr.hpp:82-87; vbsr.cpp:167-201), cpu_reference.cpp.
+// Validates the matrix (and non-negative scalar offset starts), then writes
+// C (c_len == scalar_rows * rhs floats) from B (b_len == scalar_cols * rhs).
+void cpu_reference(const vbsr_host_view& m, const float* b, int64_t b_len, int rhs, float* c, int64_t c_len);
+
 // ---- row schedule (schedule.cpp) -------------------------------------------
 
 // XCDs of an MI355X.  Workgroups are dispatched to XCDs round-robin by index.
@@ -119,15 +124,18 @@ inline bool supported_rhs(int rhs) { return rhs == 8 || rhs == 16 || rhs == 32 |
 // __restrict__ contract, row_owned.cu:12-13).  Checked on the host before
 // every launch, so a null, misaligned or aliased panel is an invalid
 // argument, not a device fault or corrupted output.
-inline void check_panels(const vbsr_device_view& a, const float* b, const float* c, int rhs) {
+inline void check_panels(int64_t scalar_rows, int64_t scalar_cols, const float* b, const float* c, int rhs) {
   if (b == nullptr || c == nullptr) throw std::invalid_argument("B and C must be device pointers");
   const uintptr_t b0 = reinterpret_cast<uintptr_t>(b);
   const uintptr_t c0 = reinterpret_cast<uintptr_t>(c);
   if (b0 % alignof(float) != 0 || c0 % alignof(float) != 0)
     throw std::invalid_argument("B and C must be 4-byte aligned");
-  const uintptr_t b1 = b0 + uintptr_t(a.scalar_cols) * uintptr_t(rhs) * sizeof(float);
-  const uintptr_t c1 = c0 + uintptr_t(a.scalar_rows) * uintptr_t(rhs) * sizeof(float);
+  const uintptr_t b1 = b0 + uintptr_t(scalar_cols) * uintptr_t(rhs) * sizeof(float);
+  const uintptr_t c1 = c0 + uintptr_t(scalar_rows) * uintptr_t(rhs) * sizeof(float);
   if (b0 < c1 && c0 < b1) throw std::invalid_argument("B and C overlap");
+}
+inline void check_panels(const vbsr_device_view& a, const float* b, const float* c, int rhs) {
+  check_panels(a.scalar_rows, a.scalar_cols, b, c, rhs);
 }
 
 // Order-preserving kernel (row_owned_scalar.hip).
