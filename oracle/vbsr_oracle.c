@@ -24,9 +24,16 @@
  *   orc_cpu_reference_threads bit-identical to orc_cpu_reference (each
  *                             row's arithmetic is unchanged; rows run in
  *                             parallel).
+ *   orc_abs_product_sum(_threads)  the dense product of |A| and |B|
+ *                             (brute force); the threaded form bit-identical
+ *                             to the serial one.
  *   orc_fmaf_order            same checks as orc_cpu_reference within fp32
- *                             tolerance; bit-exact emulation pins the GPU
- *                             order-preserving kernel.
+ *                             tolerance, plus closed forms whose bits differ
+ *                             with k order, block order and fusion (one row
+ *                             summing 2^24, 1, -2^24 gives 0 only in order;
+ *                             -(1+2^-11) + (1+2^-12)^2 gives 2^-24 only
+ *                             fused and in order); bit-exact emulation pins
+ *                             the GPU order-preserving kernel.
  *   orc_make_random_input     C++ standard known answer for mt19937 and
  *                             libstdc++'s stream.
  */
@@ -368,26 +375,37 @@ int orc_cpu_reference_threads(const orc_view* a, const float* b, int64_t b_len, 
   return ORC_OK;
 }
 
-int orc_abs_product_sum(const orc_view* a, const float* b, int64_t b_len, int32_t rhs, double* bound) {
-  const int64_t M = scalar_rows(a), K = scalar_cols(a);
-  if (b_len != K * rhs) return ORC_INVALID;
-  memset(bound, 0, sizeof(double) * (size_t)(M * rhs));
-  for (int32_t i = 0; i < a->block_rows; ++i) {
-    const int32_t h = a->row_size[i];
-    for (int32_t blk = a->row_ptr[i]; blk < a->row_ptr[i + 1]; ++blk) {
-      const int32_t col = a->block_col[blk];
-      const int32_t w = a->col_size[col];
-      const float* A = a->values + a->value_off[blk];
-      for (int32_t r = 0; r < h; ++r) {
-        for (int32_t n = 0; n < rhs; ++n) {
-          const float* Bn = b + a->col_scalar_off[col] + (int64_t)n * K;
-          double sum = 0.0;
-          for (int32_t k = 0; k < w; ++k) sum += fabs((double)A[r + (int64_t)k * h]) * fabs((double)Bn[k]);
-          bound[a->row_scalar_off[i] + r + (int64_t)n * M] += sum;
-        }
+/* Sum |a||b| of one block row's outputs (the elementwise error scale). */
+static void abs_product_row(const orc_view* a, const float* b, int32_t rhs, int64_t M, int64_t K, int32_t i,
+                            double* bound) {
+  const int32_t h = a->row_size[i];
+  for (int32_t blk = a->row_ptr[i]; blk < a->row_ptr[i + 1]; ++blk) {
+    const int32_t col = a->block_col[blk];
+    const int32_t w = a->col_size[col];
+    const float* A = a->values + a->value_off[blk];
+    for (int32_t r = 0; r < h; ++r) {
+      for (int32_t n = 0; n < rhs; ++n) {
+        const float* Bn = b + a->col_scalar_off[col] + (int64_t)n * K;
+        double sum = 0.0;
+        for (int32_t k = 0; k < w; ++k) sum += fabs((double)A[r + (int64_t)k * h]) * fabs((double)Bn[k]);
+        bound[a->row_scalar_off[i] + r + (int64_t)n * M] += sum;
       }
     }
   }
+}
+
+int orc_abs_product_sum(const orc_view* a, const float* b, int64_t b_len, int32_t rhs, double* bound) {
+  return orc_abs_product_sum_threads(a, b, b_len, rhs, 1, bound);
+}
+
+int orc_abs_product_sum_threads(const orc_view* a, const float* b, int64_t b_len, int32_t rhs, int32_t threads,
+                                double* bound) {
+  const int64_t M = scalar_rows(a), K = scalar_cols(a);
+  if (b_len != K * rhs || threads < 1) return ORC_INVALID;
+  memset(bound, 0, sizeof(double) * (size_t)(M * rhs));
+  const int32_t rows = a->block_rows;
+#pragma omp parallel for schedule(dynamic, 16) num_threads(threads)
+  for (int32_t i = 0; i < rows; ++i) abs_product_row(a, b, rhs, M, K, i, bound);
   return ORC_OK;
 }
 

@@ -141,6 +141,11 @@ int orc_cpu_reference_threads(const orc_view* a, const float* b, int64_t b_len, 
  * scale of the elementwise error bound. */
 int orc_abs_product_sum(const orc_view* a, const float* b, int64_t b_len, int32_t rhs,
                         double* bound);
+/* The same over `threads` OpenMP threads (rows in parallel, each row's sums
+ * unchanged): bit-identical to orc_abs_product_sum.  ORC_INVALID for a wrong
+ * B length or threads < 1. */
+int orc_abs_product_sum_threads(const orc_view* a, const float* b, int64_t b_len, int32_t rhs, int32_t threads,
+                                double* bound);
 
 /* Emulates the reference kernels' accumulation order bit for bit
  * (src/kernels/row_owned.cu:24-43): acc = 0.f; for each block of the row in

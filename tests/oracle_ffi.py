@@ -82,6 +82,9 @@ def lib():
         L.orc_cpu_reference_threads.argtypes = [ctypes.POINTER(OrcView), ctypes.POINTER(ctypes.c_float),
                                                 ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
                                                 ctypes.POINTER(ctypes.c_float)]
+        L.orc_abs_product_sum_threads.argtypes = [ctypes.POINTER(OrcView), ctypes.POINTER(ctypes.c_float),
+                                                  ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
+                                                  ctypes.POINTER(ctypes.c_double)]
         L.orc_make_random_input.argtypes = [ctypes.c_int64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_float)]
         L.orc_useful_flops.restype = ctypes.c_double
         L.orc_useful_flops.argtypes = [ctypes.POINTER(OrcView), ctypes.c_int32]
@@ -220,6 +223,19 @@ def fmaf_order(matrix, b, rhs):
 
 def abs_product_sum(matrix, b, rhs):
     return _product("orc_abs_product_sum", matrix, b, rhs, np.float64)
+
+
+def abs_product_sum_threads(matrix, b, rhs, threads):
+    """abs_product_sum with block rows spread over `threads` OpenMP threads; bit-identical to it."""
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    out = np.empty(matrix.scalar_rows * rhs, dtype=np.float64)
+    view = matrix.view()
+    status = lib().orc_abs_product_sum_threads(ctypes.byref(view), b.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                               len(b), rhs, threads,
+                                               out.ctypes.data_as(ctypes.POINTER(ctypes.c_double)))
+    if status != 0:
+        raise ValueError("B size or thread count")
+    return out
 
 
 def make_random_input(count, seed):

@@ -21,6 +21,8 @@ import pytest
 
 import oracle_ffi as o
 import varblockspmm_amd as vb
+from reference_cases import reference_cases
+import test_oracle
 
 torch = pytest.importorskip("torch")
 
@@ -95,19 +97,6 @@ class Case:
 
     def close(self):
         self.matrix.close()
-
-
-def reference_cases():
-    """tests/test_main.cpp:145-161: 4 distributions x degree {1,4,8,16} x RHS {8,16,32,64};
-    9 x 17 block grid; seed 11.. in order; local columns iff the seed is odd."""
-    cases = []
-    seed = 11
-    for distribution in ("uniform", "low", "high", "bimodal"):
-        for degree in (1, 4, 8, 16):
-            for rhs in (8, 16, 32, 64):
-                cases.append((distribution, degree, rhs, "local" if seed & 1 else "random", seed))
-                seed += 1
-    return cases
 
 
 @pytest.mark.parametrize("case", reference_cases(), ids=lambda c: "{}-d{}-n{}-{}-s{}".format(*c))
@@ -207,11 +196,18 @@ def test_entry_points_reject_overlapping_panels():
     b = storage[:b_count]
     overlapping_c = storage[b_count - 4:b_count - 4 + c_count]
     plan = vb.Plan(c.matrix, rhs)
+    csr = vb.ScalarCsrPlan(c.host, rhs)
+    grouped = vb.GroupedGemmPlan(c.host, rhs)
     for run in (lambda: vb.launch_row_owned(view, schedule, b, overlapping_c, rhs, c.stream),
                 lambda: vb.launch_row_owned_scalar(view, b, overlapping_c, rhs, c.stream),
-                lambda: plan.execute(b, overlapping_c, c.stream)):
+                lambda: plan.execute(b, overlapping_c, c.stream),
+                lambda: csr.execute(b, overlapping_c, c.stream),
+                lambda: grouped.execute(b, overlapping_c, c.stream)):
         with pytest.raises(ValueError, match="overlap"):
             run()
+    assert csr.workspace_bytes() == 0  # refused before the first execute set anything up
+    csr.close()
+    grouped.close()
     with pytest.raises(ValueError, match="device pointers"):
         plan.execute(None, c.c_dev, c.stream)
     # The same storage split without overlap runs, and matches the oracle.
@@ -378,6 +374,26 @@ def test_unused_b_entries_never_reach_c(rhs):
     c.close()
 
 
+@pytest.mark.parametrize("probe", test_oracle.order_probes(), ids=lambda p: p[0])
+def test_order_preserving_kernel_gives_the_closed_form_bits(probe):
+    """launch_row_owned_scalar on inputs whose bits depend on the summation order and on fusion: only
+    blocks in row_ptr order, k ascending and one fused multiply-add per term give these bits (the
+    closed forms are derived in tests/test_oracle.py, independently of the emulation)."""
+    name, m, b, rhs, want_fmaf, want_reference = probe
+    note(f"order probe {name}")
+    host = vb.HostMatrix(m.block_rows, m.block_cols, **{n: getattr(m, n) for n in o.HostMatrix.FIELDS})
+    c = Case(host, rhs, 1)
+    c.b = b.copy()
+    c.b_dev = torch.from_numpy(c.b).to(DEVICE)
+    np.testing.assert_array_equal(c.run_scalar(), want_fmaf)
+    np.testing.assert_array_equal(vb.cpu_reference(host, b, rhs), want_reference)
+    # The MFMA plan sums in its own order: on inputs built to cancel, only the elementwise bound
+    # (|C - Cref| <= 1e-6 * sum |a||b|) is meaningful.
+    result = c.run_plan(vb.Plan(c.matrix, rhs))
+    assert np.all(np.abs(result.astype(np.float64) - c.reference) <= ELEMENTWISE_TOL * c.bound), name
+    c.close()
+
+
 def test_device_matrix_errors():
     note("device errors")
     host = vb.generate(6, 6, 2, "high", "random", 1)
@@ -523,18 +539,22 @@ def test_grouped_gemm_plan_config3_and_empty_rows():
 # ---- the largest B offsets ------------------------------------------------
 
 def largest_offset_case(scalar_cols, rhs):
-    """Three block rows over scalar_cols / 64 block columns of width 64, using the first, a middle
-    and the last block column, and a B panel (ld = scalar_cols) that is zero except where those
-    columns are read.  The panel is scalar_cols * rhs floats (4.6-4.9 GB); np.zeros leaves its
-    untouched pages unallocated on the host."""
-    ncols = scalar_cols // 64
-    host = hand_made([16, 40, 8], [64] * ncols, [[0, ncols - 1], [ncols // 2], [ncols - 1]], seed=5)
+    """Three block rows over scalar_cols / 64 - 1 block columns of width 64 followed by one of 24 and
+    one of 40, using the first, a middle and the last (40-wide) block column, and a B panel
+    (ld = scalar_cols) that is zero except where those columns are read.  The last block column ends
+    at scalar_cols, so its 8-column half step reads the panel's last B rows at every RHS column: the
+    largest offsets of both step kinds.  The panel is scalar_cols * rhs floats (4.6-4.9 GB);
+    np.zeros leaves its untouched pages unallocated on the host."""
+    ncols = scalar_cols // 64 + 1
+    col_size = [64] * (ncols - 2) + [24, 40]
+    assert sum(col_size) == scalar_cols
+    host = hand_made([16, 40, 8], col_size, [[0, ncols - 1], [ncols // 2], [ncols - 1]], seed=5)
     rng = np.random.default_rng(9)
     b = np.zeros(scalar_cols * rhs, dtype=np.float32)
     for col in sorted({0, ncols // 2, ncols - 1}):
+        start, end = int(host.col_scalar_off[col]), int(host.col_scalar_off[col + 1])
         for n in range(rhs):
-            start = n * scalar_cols + col * 64
-            b[start:start + 64] = rng.uniform(-1, 1, 64).astype(np.float32)
+            b[n * scalar_cols + start:n * scalar_cols + end] = rng.uniform(-1, 1, end - start).astype(np.float32)
     return host, b
 
 

@@ -1,5 +1,8 @@
-"""GPU parity over the whole regime sweep, at a reduced size, plus the
-benchmark executable and the sweep runner end to end.
+"""GPU parity over the whole regime sweep, at its full size and at a reduced
+size, plus the benchmark executable and the sweep runner end to end.
+
+Configuration 5's 128 cases run at their own size (4096 block rows) against
+the threaded oracle.
 
 Every case of both grids (the 128-case config-5 sweep, with seed = case
 index, and the reference's publication grid) is generated at 48 block rows
@@ -14,11 +17,12 @@ import os
 import subprocess
 import sys
 
+import numpy as np
 import pytest
 
 import oracle_ffi as o
 import varblockspmm_amd as vb
-from test_gpu_parity import Case, note
+from test_gpu_parity import ELEMENTWISE_TOL, NORMWISE_TOL, REL_L2_TOL, Case, note
 
 torch = pytest.importorskip("torch")
 
@@ -55,6 +59,52 @@ def test_sweep_case_parity(grid, index, case):
             assert scalar.tobytes() == expected.tobytes(), "order-preserving kernel differs from fmaf order"
     finally:
         c.close()
+
+
+FULL_ROWS = 4096
+THREADS = max(1, min(16, int(os.environ.get("OMP_NUM_THREADS", "8"))))
+CONFIG5 = list(enumerate(run_grid.cases("config5")))
+
+
+@pytest.mark.parametrize("index,case", CONFIG5,
+                         ids=[f"{i}-{c['distribution']}-{c['locality']}-d{c['degree']}-n{c['rhs']}" for i, c in CONFIG5])
+def test_config5_full_size_parity(index, case):
+    """BASELINE configuration 5 at its own size: each of the 128 cases at 4096 block rows (the generator
+    makes a different matrix at another row count, not a smaller copy), Plan::execute checked against the
+    oracle's cpu_reference (rows over OpenMP threads, bit-identical to the serial one) with the bars of
+    test_gpu_parity.py, and bit-stable across two runs.  B is the reference test's generator with the
+    case's seed."""
+    rhs, seed = case["rhs"], case["seed"]
+    note(f"config5 full size case {index}: {case}")
+    host = vb.generate(FULL_ROWS, FULL_ROWS, case["degree"], case["distribution"], case["locality"], seed)
+    oracle = o.HostMatrix(host.block_rows, host.block_cols, **host.arrays())
+    b = o.make_random_input(host.scalar_cols * rhs, seed)
+    matrix = vb.Matrix(host)
+    try:
+        stream = torch.cuda.Stream(device="cuda:0")
+        b_dev = torch.from_numpy(b).to("cuda:0")
+        c_dev = torch.full((host.scalar_rows * rhs,), float("nan"), device="cuda:0")
+        plan = vb.Plan(matrix, rhs)
+        runs = []
+        for _ in range(2):
+            c_dev.fill_(float("nan"))
+            torch.cuda.synchronize()
+            with torch.cuda.stream(stream):
+                plan.execute(b_dev, c_dev, stream)
+            stream.synchronize()
+            runs.append(c_dev.cpu().numpy())
+        plan.close()
+        assert runs[0].tobytes() == runs[1].tobytes(), "plan not bit-stable"
+        result = runs[0]
+        assert np.all(np.isfinite(result)), "NaN/Inf (unwritten or polluted outputs)"
+        reference = o.cpu_reference_threads(oracle, b, rhs, THREADS)
+        bound = o.abs_product_sum_threads(oracle, b, rhs, THREADS)
+        max_abs, rel_l2, normwise, elementwise = o.parity_errors(result, reference, bound)
+        note(f"  max_abs={max_abs:.3g} rel_l2={rel_l2:.3g} normwise={normwise:.3g} elementwise={elementwise:.3g}")
+        assert max_abs <= 5e-4 and rel_l2 <= 5e-5  # tests/test_main.cpp:35
+        assert normwise <= NORMWISE_TOL and rel_l2 <= REL_L2_TOL and elementwise <= ELEMENTWISE_TOL
+    finally:
+        matrix.close()
 
 
 def test_benchmark_executable_end_to_end():

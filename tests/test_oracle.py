@@ -328,9 +328,11 @@ def test_threaded_cpu_reference_is_bit_identical(threads):
         m = o.generate(*args)
         b = o.make_random_input(m.scalar_cols * rhs, args[-1])
         np.testing.assert_array_equal(o.cpu_reference_threads(m, b, rhs, threads), o.cpu_reference(m, b, rhs))
+        np.testing.assert_array_equal(o.abs_product_sum_threads(m, b, rhs, threads), o.abs_product_sum(m, b, rhs))
     m = _rows_with_empty()
     b = o.make_random_input(m.scalar_cols * 8, 3)
     np.testing.assert_array_equal(o.cpu_reference_threads(m, b, 8, threads), o.cpu_reference(m, b, 8))
+    np.testing.assert_array_equal(o.abs_product_sum_threads(m, b, 8, threads), o.abs_product_sum(m, b, 8))
     with pytest.raises(ValueError):
         o.cpu_reference_threads(m, b[:-1], 8, threads)
     with pytest.raises(ValueError):
@@ -421,3 +423,88 @@ def test_make_random_input_stream():
 def test_useful_flops():
     m = o.generate(10, 10, 3, "high", "random", seed=2)
     assert o.useful_flops(m, 32) == 2 * 32 * m.sum_hw()
+
+
+# ---- the fmaf order itself: inputs whose bits depend on the order and on fusion ----------------------------
+
+BIG = np.float32(2.0 ** 24)
+
+
+def _one_row(blocks, col_widths, h=8):
+    """One block row of height h whose blocks (h x w value arrays, column-major) sit in block columns 0, 1, ...
+    of widths col_widths."""
+    values = np.concatenate([np.asarray(v, np.float32).reshape(-1, order="F") for v in blocks])
+    sizes = [np.asarray(v).size for v in blocks]
+    col_widths = np.asarray(col_widths)
+    return o.HostMatrix(1, len(col_widths), row_ptr=[0, len(blocks)], block_col=np.arange(len(blocks)),
+                        row_size=[h], col_size=col_widths, row_scalar_off=[0, h],
+                        col_scalar_off=np.concatenate([[0], np.cumsum(col_widths)]),
+                        value_off=np.concatenate([[0], np.cumsum(sizes)]), values=values)
+
+
+def order_probes():
+    """(name, matrix, B, rhs, fmaf-order C, cpu_reference C): closed forms whose bits differ by summation
+    order or by fusion, so that an emulation (or kernel) with k reversed, blocks reversed or multiply and
+    add rounded separately gives other bits.  2^24 + 1 rounds to 2^24 (tie to even) while 1 - 2^24 is exact;
+    (1 + 2^-12)^2 = 1 + 2^-11 + 2^-24 is exact only inside a fused multiply-add."""
+    probes = []
+    rhs = 8
+    # k order within a block: rows 0-2 of one 8 x 8 block, B = 1.
+    a = np.zeros((8, 8), np.float32)
+    a[0, :3] = [BIG, 1, -BIG]
+    a[1, :3] = [-BIG, 1, BIG]
+    a[2, :3] = [1, BIG, -BIG]
+    m = _one_row([a], [8])
+    b = np.ones(8 * rhs, np.float32)
+    fm = np.zeros((rhs, 8), np.float32)
+    fm[:, 1] = 1  # in k order: 0, 1, 0; reversed: 1, 0, 1
+    ref = np.zeros((rhs, 8), np.float32)
+    ref[:, :3] = 1  # each block's sum is exact in double
+    probes.append(("k-order", m, b, rhs, fm.reshape(-1), ref.reshape(-1)))
+    # Block order: three 8 x 8 blocks, the values in column 0 of each.
+    blocks = [np.zeros((8, 8), np.float32) for _ in range(3)]
+    for row, vals in ((0, (BIG, 1, -BIG)), (1, (-BIG, 1, BIG))):
+        for blk, v in zip(blocks, vals):
+            blk[row, 0] = v
+    m = _one_row(blocks, [8, 8, 8])
+    b = np.ones(24 * rhs, np.float32)
+    fm = np.zeros((rhs, 8), np.float32)
+    fm[:, 1] = 1  # blocks in row_ptr order: 0, 1; reversed: 1, 0
+    probes.append(("block-order", m, b, rhs, fm.reshape(-1), fm.reshape(-1).copy()))
+    # Fusion: A row 0 = [-(1 + 2^-11), 1 + 2^-12], B column = [1, 1 + 2^-12, 0, ...].
+    a = np.zeros((8, 8), np.float32)
+    a[0, :2] = [-(1 + 2.0 ** -11), 1 + 2.0 ** -12]
+    m = _one_row([a], [8])
+    col = np.zeros(8, np.float32)
+    col[:2] = [1, 1 + 2.0 ** -12]
+    b = np.tile(col, rhs)
+    fm = np.zeros((rhs, 8), np.float32)
+    fm[:, 0] = 2.0 ** -24  # fused, in order; unfused or reversed: 0
+    probes.append(("fusion", m, b, rhs, fm.reshape(-1), fm.reshape(-1).copy()))
+    return probes
+
+
+@pytest.mark.parametrize("probe", order_probes(), ids=lambda p: p[0])
+def test_fmaf_order_is_pinned_by_order_and_fusion_sensitive_closed_forms(probe):
+    _, m, b, rhs, want_fmaf, want_reference = probe
+    assert o.validate(m) == 0
+    np.testing.assert_array_equal(o.fmaf_order(m, b, rhs), want_fmaf)
+    np.testing.assert_array_equal(o.cpu_reference(m, b, rhs), want_reference)
+
+
+def test_order_probes_tell_the_alternatives_apart():
+    """The probes' expected values are not what the plausible mistakes give: computed here in numpy with k
+    reversed, blocks reversed, and the multiply rounded before the add."""
+    f32 = np.float32
+
+    def chain(terms, fused=True):
+        acc = f32(0)
+        for x, y in terms:
+            acc = f32(np.float64(x) * np.float64(y) + np.float64(acc)) if fused else f32(f32(x * y) + acc)
+        return acc
+
+    row0 = [(BIG, 1), (f32(1), 1), (-BIG, 1)]
+    assert chain(row0) == 0 and chain(row0[::-1]) == 1
+    fuse = [(f32(-(1 + 2.0 ** -11)), f32(1)), (f32(1 + 2.0 ** -12), f32(1 + 2.0 ** -12))]
+    assert chain(fuse) == f32(2.0 ** -24)
+    assert chain(fuse, fused=False) == 0 and chain(fuse[::-1]) == 0
