@@ -154,7 +154,7 @@ int64_t vbsr_matrix_scalar_cols(const vbsr_matrix* matrix);
  * arrays owned by the matrix; opaque to callers. */
 typedef struct vbsr_row_schedule {
   const void* steps;     /* device: one 16-byte record per k step */
-  const void* rows;      /* device: one 96-byte row item per workgroup, launch order for rhs 8 and 16 */
+  const void* rows;      /* device: four 48-byte wave items per workgroup, launch order for rhs 8 and 16 */
   int64_t groups;        /* workgroups of one launch */
   int32_t step_limit;    /* index of the last step record */
   const void* rows_wide; /* device: the same row items, launch order for rhs 32 and 64 */

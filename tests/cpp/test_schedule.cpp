@@ -2,13 +2,15 @@
 // from the library's own sources without a GPU.  For each matrix:
 //   * the step records cover every block of every row exactly once, in
 //     row_ptr order, with the A and B offsets the kernel reads;
-//   * both launch orders hold every block row once, padding slots have
-//     step_count < 0, and each row item describes its row, including each
-//     wave's first step record;
+//   * both launch orders hold every block row once, in workgroups of four
+//     wave items: one shared row (rows of more than kPackSteps steps) or up
+//     to four packed light rows, one per wave; padding waves have
+//     step_count < 0; each item describes its row, including the wave's
+//     first step record;
 //   * both orders place each row on the same XCD (workgroup index mod 8), and
 //     no XCD's work exceeds an eighth of the total by more than one row's;
-//   * `rows` runs each XCD's rows heaviest first; `rows_wide` ends each XCD's
-//     band with its lightest quarter, heaviest first;
+//   * `rows` runs each XCD's workgroups heaviest first; `rows_wide` ends each
+//     XCD's band with its lightest quarter, heaviest first;
 //   * building twice gives the same schedule;
 //   * matrices whose rows share few block columns (every row on the same 8
 //     columns; rows overlapping in 15 of 16 columns) build in seconds: the
@@ -38,42 +40,70 @@ int failures = 0;
     }                                                                            \
   } while (0)
 
-int64_t row_work(const vbsr_amd::RowItem& item) {
-  return int64_t((item.h + 15) / 16) * item.step_count + 8;
-}
+int64_t row_work(const vbsr_amd::WaveItem& item) { return int64_t((item.h + 15) / 16) * item.step_count; }
 
-void check_order(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s, const std::vector<vbsr_amd::RowItem>& items,
-                 std::vector<int>& xcd_of_row, bool wide) {
+// Checks one launch order: kRowWaves items per workgroup, each workgroup
+// either one shared row (every wave, lead = wave, each wave's first step
+// record), or up to kRowWaves packed light rows (one per wave, then idle
+// waves), or padding (all idle); every block row exactly once; each row on
+// the same XCD in both orders; per-XCD work within an eighth plus one
+// workgroup; the order of each XCD's workgroups.
+void check_order(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s,
+                 const std::vector<vbsr_amd::WaveItem>& items, std::vector<int>& xcd_of_row, bool wide) {
+  using vbsr_amd::kPackSteps;
+  using vbsr_amd::kRowWaves;
   using vbsr_amd::kXcds;
-  CHECK(int64_t(items.size()) == s.groups);
+  CHECK(int64_t(items.size()) == s.groups * kRowWaves);
   CHECK(s.groups % kXcds == 0);
   std::vector<int> seen(size_t(m.block_rows), 0);
   std::vector<int64_t> load(kXcds, 0);
   std::vector<std::vector<int64_t>> band_work(kXcds);
   bool padding_started[kXcds] = {};
   for (int64_t g = 0; g < s.groups; ++g) {
-    const auto& item = items[size_t(g)];
+    const auto* wg = &items[size_t(g) * kRowWaves];
     const int xcd = int(g % kXcds);
-    if (item.step_count < 0) {
+    if (wg[0].step_count < 0) {
+      for (int w = 0; w < kRowWaves; ++w) CHECK(wg[w].step_count < 0);
       padding_started[xcd] = true;
       continue;
     }
-    CHECK(!padding_started[xcd]);  // padding only after an XCD's last row
-    const int32_t i = item.row;
-    CHECK(i >= 0 && i < m.block_rows);
-    CHECK(++seen[size_t(i)] == 1);
-    CHECK(item.c_off == m.row_scalar_off[i]);
-    CHECK(item.h == m.row_size[i]);
-    for (int w = 0; w < vbsr_amd::kRowWaves; ++w) {
-      const int32_t step = item.step_first + vbsr_amd::kStepRun * w;
-      const bool has = vbsr_amd::kStepRun * w < item.step_count;
-      CHECK(item.first[w].a_off == (has ? s.steps[size_t(step)].a_off : 0));
-      CHECK(item.first[w].b_off == (has ? s.steps[size_t(step)].b_off : 0));
+    CHECK(!padding_started[xcd]);  // padding only after an XCD's last workgroup
+    int64_t work = 8;
+    const bool shared = wg[0].group == kRowWaves;
+    bool idle_seen = false;
+    for (int w = 0; w < kRowWaves; ++w) {
+      const auto& item = wg[w];
+      if (!shared && item.step_count < 0) {
+        idle_seen = true;
+        continue;
+      }
+      CHECK(!idle_seen);  // a packed workgroup's idle waves come last
+      const int32_t i = item.row;
+      CHECK(i >= 0 && i < m.block_rows);
+      CHECK(item.c_off == m.row_scalar_off[i]);
+      CHECK(item.h == m.row_size[i]);
+      int32_t first;
+      if (shared) {
+        CHECK(item.group == kRowWaves && item.lead == w && item.row == wg[0].row);
+        CHECK(item.step_count > kPackSteps);
+        first = item.step_first + vbsr_amd::kStepRun * w;
+      } else {
+        CHECK(item.group == 1 && item.lead == 0);
+        CHECK(item.step_count <= kPackSteps);
+        first = item.step_first;
+      }
+      const bool has = first < item.step_first + item.step_count;
+      CHECK(item.first.a_off == (has ? s.steps[size_t(first)].a_off : 0));
+      CHECK(item.first.b_off == (has ? s.steps[size_t(first)].b_off : 0));
+      if (!shared || w == 0) {
+        CHECK(++seen[size_t(i)] == 1);
+        work += row_work(item);
+        if (xcd_of_row[size_t(i)] < 0) xcd_of_row[size_t(i)] = xcd;
+        CHECK(xcd_of_row[size_t(i)] == xcd);
+      }
     }
-    if (xcd_of_row[size_t(i)] < 0) xcd_of_row[size_t(i)] = xcd;
-    CHECK(xcd_of_row[size_t(i)] == xcd);
-    load[size_t(xcd)] += row_work(item);
-    band_work[size_t(xcd)].push_back(row_work(item));
+    load[size_t(xcd)] += work;
+    band_work[size_t(xcd)].push_back(work);
   }
   for (int32_t i = 0; i < m.block_rows; ++i) CHECK(seen[size_t(i)] == 1);
   int64_t heaviest = 0;
@@ -97,9 +127,9 @@ void check_order(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s, const
 
 void check_steps(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s) {
   const auto& items = s.rows;
-  std::vector<const vbsr_amd::RowItem*> by_row(size_t(m.block_rows), nullptr);
+  std::vector<const vbsr_amd::WaveItem*> by_row(size_t(m.block_rows), nullptr);
   for (const auto& item : items)
-    if (item.step_count >= 0) by_row[size_t(item.row)] = &item;
+    if (item.step_count >= 0 && item.lead == 0) by_row[size_t(item.row)] = &item;
   int64_t expected_first = 0;
   for (int32_t i = 0; i < m.block_rows; ++i) {
     const auto* item = by_row[size_t(i)];
@@ -129,7 +159,7 @@ void check_steps(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s) {
   CHECK(int64_t(s.steps.size()) == expected_first);
 }
 
-bool same(const std::vector<vbsr_amd::RowItem>& a, const std::vector<vbsr_amd::RowItem>& b) {
+bool same(const std::vector<vbsr_amd::WaveItem>& a, const std::vector<vbsr_amd::WaveItem>& b) {
   return a.size() == b.size() && (a.empty() || std::memcmp(a.data(), b.data(), a.size() * sizeof(a[0])) == 0);
 }
 

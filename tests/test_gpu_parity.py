@@ -327,6 +327,12 @@ EDGE_MATRICES = {
     "all-64": lambda: hand_made([64] * 12, [64] * 12, [[(i * 5 + j) % 12 for j in range(4)] for i in range(12)]),
     "narrow-wide": lambda: hand_made([8, 64] * 8, [64, 8] * 8, [[j for j in range(16) if (i + j) % 3 == 0]
                                                                  for i in range(16)]),
+    # rows of 0-4 k steps (packed four to a workgroup, one per wave, of every height) beside rows of 5 and 7
+    # steps (one workgroup each); 11 light rows leave a packed workgroup with idle waves
+    "packed-light": lambda: hand_made([8, 16, 24, 32, 40, 48, 56, 64, 64, 8, 40, 16, 24, 56],
+                                      [8, 16, 24, 64, 40],
+                                      [[], [0], [2], [0, 1, 2], [3], [3, 0], [4], [1, 4], [2, 2], [3, 4], [1], [0, 0],
+                                       [4, 0], []]),
     # 100 blocks of width 64 in one row: 400 k steps, more than one workgroup
     # segment holds (256), so the row is accumulated across segments
     "long-row": lambda: hand_made([16, 40, 8], [64] * 100 + [8] * 20,

@@ -54,42 +54,51 @@ struct alignas(16) StepRec {
 static_assert(sizeof(StepRec) == 16, "StepRec is read as one dwordx4");
 constexpr int64_t kHalfStep = int64_t(1) << 62;
 
-// The row-owned kernel's workgroup: kRowWaves waves share a row's k steps,
-// dealt in runs of kStepRun consecutive steps (wave w's first step is the
-// row's step kStepRun * w).
+// The row-owned kernel's workgroup: kRowWaves waves.  They hold either one
+// block row together -- its k steps dealt to the waves in runs of kStepRun
+// consecutive steps (wave w's first step is the row's step kStepRun * w) and
+// their partial tiles summed in LDS -- or up to kRowWaves light rows of at
+// most kPackSteps steps, one per wave, with no reduction.
 constexpr int kRowWaves = 4;
 constexpr int kStepRun = 2;
+constexpr int kPackSteps = 4;
 
-// One workgroup's work: block row `row`, whose steps are
-// steps[step_first .. step_first + step_count).  A padding slot has
-// step_count < 0.  first[w] repeats wave w's first step record (zero when
-// the wave has none), so the kernel can issue that step's loads as soon as
-// the row item arrives instead of after the step records.  96 bytes, read
-// with scalar loads.
-struct alignas(32) RowItem {
+// One wave's work: its share of block row `row`, whose steps are
+// steps[step_first .. step_first + step_count).  `group` waves share the row
+// (kRowWaves, or 1 for a packed light row) and this wave is the `lead`-th of
+// them.  An idle wave (a packed workgroup with fewer than kRowWaves rows, or
+// a padding workgroup) has step_count < 0.  `first` repeats the wave's first
+// step record (zero when it has none), so the kernel can issue that step's
+// loads as soon as the item arrives instead of after the step records.
+// 48 bytes, read with scalar loads; a workgroup's kRowWaves items are
+// consecutive.
+struct alignas(16) WaveItem {
   int64_t c_off;       // row_scalar_off[row]: first row of C written
   int32_t step_first;  // index of the row's first StepRec
-  int32_t step_count;  // the row's k steps; < 0 for a padding slot
+  int32_t step_count;  // the row's k steps; < 0 for an idle wave
   int32_t h;           // row_size[row]: leading dimension of the row's blocks
-  int32_t row;         // block row (diagnostics only)
-  int32_t pad0, pad1;
-  StepRec first[kRowWaves];
+  int32_t row;         // block row (diagnostics only; -1 when idle)
+  int32_t group;       // waves sharing the row: kRowWaves or 1
+  int32_t lead;        // this wave's index among them
+  StepRec first;
 };
-static_assert(sizeof(RowItem) == 96, "RowItem is read as 24 dwords");
+static_assert(sizeof(WaveItem) == 48, "WaveItem is read as 12 dwords");
 
 struct HostSchedule {
-  std::vector<StepRec> steps;      // row after row, blocks in row_ptr order
-  std::vector<RowItem> rows;       // one per workgroup, launch order for RHS 8 and 16
-  std::vector<RowItem> rows_wide;  // the same items, launch order for RHS 32 and 64
-  int64_t groups{};                // workgroups of one launch (multiple of kXcds)
+  std::vector<StepRec> steps;       // row after row, blocks in row_ptr order
+  std::vector<WaveItem> rows;       // kRowWaves per workgroup, launch order for RHS 8 and 16
+  std::vector<WaveItem> rows_wide;  // the same workgroups, launch order for RHS 32 and 64
+  int64_t groups{};                 // workgroups of one launch (multiple of kXcds)
 };
 
-// Step records plus two launch orders of the block rows.  Both place each row
-// on the XCD whose eighth of the block columns holds most of its block widths
-// (so an XCD's B slices concentrate in one eighth of B), with equal work per
-// XCD.  Within an XCD, `rows` runs the heaviest rows first; `rows_wide` chains
-// rows that share block columns and keeps the lightest quarter last.
-// Deterministic.
+// Step records plus two launch orders of the workgroups.  Rows of at most
+// kPackSteps steps are packed kRowWaves to a workgroup (rows of similar work
+// together); every other row has a workgroup of its own.  Both orders place
+// each workgroup on the XCD whose eighth of the block columns holds most of
+// its rows' block widths (so an XCD's B slices concentrate in one eighth of
+// B), with equal work per XCD.  Within an XCD, `rows` runs the heaviest
+// workgroups first; `rows_wide` chains workgroups whose rows share block
+// columns and keeps the lightest quarter last.  Deterministic.
 HostSchedule build_schedule(const vbsr_host_view& host);
 
 // ---- device format (device_matrix.cpp) ----------------------------------

@@ -3,16 +3,18 @@
 // (src/kernels/row_owned.cu:47-310, dispatched at 397-423).
 //
 // Work unit.  One workgroup (4 waves) owns one block row of height h and
-// writes its h x RHS slab of C; nothing else writes it, so there are no
-// atomics and no global workspace.  The row's k steps (16 columns of one
-// block, or the 8 that end a block whose width is 8 mod 16; one precomputed
-// record each) are dealt to the four waves in runs of two; each wave
-// accumulates all T = ceil(h/16) row tiles for its steps, and the four
-// partial slabs are summed in LDS in a fixed order, (w0 + w2) + (w1 + w3):
-// at RHS 16 and 32 by wave 0 after one barrier, at RHS 8 and 64 in pairs
-// over three barriers.
-// The accumulation order depends only on the matrix, so results are
-// bit-identical from run to run.
+// writes its h x RHS slab of C, or owns up to four light rows, one per wave
+// (the schedule packs rows of at most kPackSteps k steps); nothing else
+// writes those slabs, so there are no atomics and no global workspace.  A
+// row's k steps (16 columns of one block, or the 8 that end a block whose
+// width is 8 mod 16; one precomputed record each) are dealt to the waves
+// that share it -- four, in runs of two, or a packed row's one wave; each
+// wave accumulates all T = ceil(h/16) row tiles for its steps.  The four
+// partial slabs of a shared row are summed in LDS in a fixed order,
+// (w0 + w2) + (w1 + w3): at RHS 16 and 32 by wave 0 after one barrier, at
+// RHS 8 and 64 in pairs over three barriers.  A packed row's wave stores its
+// sums itself.  The accumulation order depends only on the matrix, so
+// results are bit-identical from run to run.
 //
 // Arithmetic.  v_mfma_f32_16x16x4_f32 on transposed 16x16 output tiles,
 //   D[n][r] = sum_k B[k, n0 + n] * A[16t + r, k],
@@ -54,7 +56,7 @@
 // faster and the A slot stays.
 //
 // Pipeline.  A wave's step records are read with one load (lane j holds its
-// j-th step); its first step's record also comes with the row item, so that
+// j-th step); its first step's record also comes with its work item, so that
 // step's loads are issued without waiting for that load.  Two register
 // stages alternate: the loads of step j + 1 are in flight while step j
 // computes.  All lane offsets are per-row constants, so
@@ -80,9 +82,6 @@ constexpr int kWaves = kRowWaves;
 constexpr int kThreads = kWave * kWaves;
 constexpr int kMaxTiles = 4;  // h <= 64
 constexpr int kRun = kStepRun;  // consecutive steps dealt to one wave
-// Steps whose records one wave holds at once (one per lane): a row is
-// processed in segments of kWaves * kWave steps.
-constexpr int kSegment = kWaves * kWave;
 constexpr int64_t kOffsetMask = kHalfStep - 1;
 // Buffer resource word 3 for raw (unformatted, unswizzled) dword access.
 constexpr int kRawBufferFlags = 0x00020000;
@@ -142,29 +141,19 @@ __device__ __forceinline__ int b_slot_index(int n, int q) {
   return n * 4 + ((q ^ (n >> 1) ^ (n >> 2)) & 3);
 }
 
-// Steps of a segment dealt to `wave`: runs r = wave, wave + 4, ... of kRun
-// steps each, the last run possibly short.
-__device__ __forceinline__ int owned_steps(int count, int wave) {
+// Steps of a segment dealt to the lead-th of the 2^shift waves sharing a row:
+// runs r = lead, lead + 2^shift, ... of kRun steps each, the last run
+// possibly short.
+__device__ __forceinline__ int owned_steps(int count, int lead, int shift) {
   const int full = count / kRun;
   const int rest = count % kRun;
-  const int full_owned = full > wave ? (full - wave + kWaves - 1) / kWaves : 0;
-  return full_owned * kRun + ((rest > 0 && full % kWaves == wave) ? rest : 0);
-}
-
-// The wave's first step of the row, which the row item carries (a switch
-// keeps the selection in scalar registers).
-__device__ __forceinline__ StepRec first_step(const RowItem& item, int wave) {
-  switch (wave) {
-  case 0: return item.first[0];
-  case 1: return item.first[1];
-  case 2: return item.first[2];
-  default: return item.first[3];
-  }
+  const int full_owned = full > lead ? (full - lead + (1 << shift) - 1) >> shift : 0;
+  return full_owned * kRun + ((rest > 0 && (full & ((1 << shift) - 1)) == lead) ? rest : 0);
 }
 
 // Index within its segment of the wave's j-th step.
-__device__ __forceinline__ int owned_step(int j, int wave) {
-  return ((j / kRun) * kWaves + wave) * kRun + j % kRun;
+__device__ __forceinline__ int owned_step(int j, int lead, int shift) {
+  return (((j / kRun) << shift) + lead) * kRun + j % kRun;
 }
 
 // One step's operands as loaded: A load q holds floats 256 q + 4 lane .. + 3
@@ -179,14 +168,77 @@ struct Stage {
 struct Launch {
   vbsr_device_view a;
   const StepRec* steps;
-  const RowItem* rows;
+  const WaveItem* items;  // kWaves per workgroup
   int32_t step_limit;  // index of the last StepRec
   const float* b;
   float* c;
 };
 
+// Fixed-order reduction of the four partial slabs of a shared row,
+// (w0 + w2) + (w1 + w3), after every wave's main loop.  Afterwards wave 0's
+// acc holds the row's sums; returns true for wave 0 only.  The whole
+// workgroup shares the row, so every wave reaches the barriers.
 template <int RHS, int T>
-__device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, char* lds, int wave, int lane) {
+__device__ __forceinline__ bool reduce_partials(f32x4 (&acc)[T][rhs_tiles<RHS>()], char* lds, int wave, int lane) {
+  using Layout = Lds<RHS>;
+  constexpr int kRhsTiles = rhs_tiles<RHS>();
+  f32x4* part1 = reinterpret_cast<f32x4*>(lds + Layout::area(1));
+  f32x4* part2 = reinterpret_cast<f32x4*>(lds + Layout::area(2));
+  f32x4* part3 = reinterpret_cast<f32x4*>(lds + Layout::area(3));
+  auto slab = [&](int t, int nt) { return (t * kRhsTiles + nt) * kWave + lane; };
+  if constexpr (Layout::kOneBarrier) {
+    // Waves 1-3 leave their slabs in their own LDS areas; wave 0 sums them.
+    if (wave > 0) {
+      f32x4* part = wave == 1 ? part1 : wave == 2 ? part2 : part3;
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int nt = 0; nt < kRhsTiles; ++nt) part[slab(t, nt)] = acc[t][nt];
+    }
+    __syncthreads();
+    if (wave != 0) return false;
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int nt = 0; nt < kRhsTiles; ++nt)
+        acc[t][nt] = (acc[t][nt] + part2[slab(t, nt)]) + (part1[slab(t, nt)] + part3[slab(t, nt)]);
+  } else {
+    // Waves 2 and 3 leave their slabs; waves 0 and 1 add them; wave 1 passes
+    // its sum to wave 0 through wave 2's area.
+    if (wave >= 2) {
+      f32x4* part = wave == 2 ? part2 : part3;
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int nt = 0; nt < kRhsTiles; ++nt) part[slab(t, nt)] = acc[t][nt];
+    }
+    __syncthreads();
+    if (wave < 2) {
+      const f32x4* part = wave == 0 ? part2 : part3;
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int nt = 0; nt < kRhsTiles; ++nt) acc[t][nt] += part[slab(t, nt)];
+    }
+    __syncthreads();
+    if (wave == 1) {
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int nt = 0; nt < kRhsTiles; ++nt) part2[slab(t, nt)] = acc[t][nt];
+    }
+    __syncthreads();
+    if (wave != 0) return false;
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int nt = 0; nt < kRhsTiles; ++nt) acc[t][nt] += part2[slab(t, nt)];
+  }
+  return true;
+}
+
+template <int RHS, int T>
+__device__ __forceinline__ void row_body(const Launch& L, const WaveItem& item, char* lds, int wave, int lane) {
   using Layout = Lds<RHS>;
   constexpr int kRhsTiles = rhs_tiles<RHS>();
   constexpr int kRhsLanes = RHS < 16 ? RHS : 16;
@@ -196,6 +248,11 @@ __device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, c
   const int h = uniform(item.h);
   const int count = uniform(item.step_count);
   const int first = uniform(item.step_first);
+  // The row is shared by all kWaves waves (lead = wave) or is this wave's own.
+  const bool shared = uniform(item.group) > 1;
+  const int lead = shared ? wave : 0;
+  const int shift = shared ? 2 : 0;
+  static_assert(kWaves == 4, "a shared row is dealt to 2^2 waves");
   const int last_rows = h - 16 * (T - 1);  // 8 or 16
   const uint32_t ldb = uint32_t(L.a.scalar_cols);
 
@@ -246,12 +303,13 @@ __device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, c
 #pragma unroll
     for (int nt = 0; nt < kRhsTiles; ++nt) acc[t][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  for (int seg = 0; seg < count; seg += kSegment) {
-    const int seg_count = min(kSegment, count - seg);
-    const int mine = owned_steps(seg_count, wave);
+  const int segment = kWave << shift;  // steps whose records the row's waves hold at once, one per lane
+  for (int seg = 0; seg < count; seg += segment) {
+    const int seg_count = min(segment, count - seg);
+    const int mine = owned_steps(seg_count, lead, shift);
     if (mine == 0) continue;
-    const StepRec rec = L.steps[min(first + seg + owned_step(min(lane, mine - 1), wave), L.step_limit)];
-    const StepRec lead = first_step(item, wave);
+    const StepRec rec = L.steps[min(first + seg + owned_step(min(lane, mine - 1), lead, shift), L.step_limit)];
+    const StepRec lead_rec = item.first;
 
     // Loads the wave's j-th step of the segment; a dead step (live == false)
     // gets zero-byte resources.  The row's first step comes from the row item,
@@ -259,8 +317,8 @@ __device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, c
     auto issue = [&](Stage<RHS, T>& st, int j, bool live) {
       const int l = min(j, kWave - 1);
       const bool leading = seg == 0 && j == 0;
-      const int64_t a_off = leading ? lead.a_off : lane_value(rec.a_off, l);
-      const int64_t b_word = leading ? lead.b_off : lane_value(rec.b_off, l);
+      const int64_t a_off = leading ? lead_rec.a_off : lane_value(rec.a_off, l);
+      const int64_t b_word = leading ? lead_rec.b_off : lane_value(rec.b_off, l);
       const bool half = (b_word & kHalfStep) != 0;
       const rsrc_t a_rsrc = make_rsrc(L.a.values + a_off, live ? (half ? a_half_bytes : a_full_bytes) : 0u);
       // The buffer-load builtins return raw bits (u32x4): bit-cast them.
@@ -321,60 +379,9 @@ __device__ __forceinline__ void row_body(const Launch& L, const RowItem& item, c
     }
   }
 
-  // Fixed-order reduction of the four partial slabs, (w0 + w2) + (w1 + w3);
-  // afterwards wave 0's acc holds the row's sums.
-  f32x4* part1 = reinterpret_cast<f32x4*>(lds + Layout::area(1));
-  f32x4* part2 = reinterpret_cast<f32x4*>(lds + Layout::area(2));
-  f32x4* part3 = reinterpret_cast<f32x4*>(lds + Layout::area(3));
-  auto slab = [&](int t, int nt) { return (t * kRhsTiles + nt) * kWave + lane; };
-  if constexpr (Layout::kOneBarrier) {
-    // Waves 1-3 leave their slabs in their own LDS areas; wave 0 sums them.
-    if (wave > 0) {
-      f32x4* part = wave == 1 ? part1 : wave == 2 ? part2 : part3;
-#pragma unroll
-      for (int t = 0; t < T; ++t)
-#pragma unroll
-        for (int nt = 0; nt < kRhsTiles; ++nt) part[slab(t, nt)] = acc[t][nt];
-    }
-    __syncthreads();
-    if (wave != 0) return;
-#pragma unroll
-    for (int t = 0; t < T; ++t)
-#pragma unroll
-      for (int nt = 0; nt < kRhsTiles; ++nt)
-        acc[t][nt] = (acc[t][nt] + part2[slab(t, nt)]) + (part1[slab(t, nt)] + part3[slab(t, nt)]);
-  } else {
-    // Waves 2 and 3 leave their slabs; waves 0 and 1 add them; wave 1 passes
-    // its sum to wave 0 through wave 2's area.
-    if (wave >= 2) {
-      f32x4* part = wave == 2 ? part2 : part3;
-#pragma unroll
-      for (int t = 0; t < T; ++t)
-#pragma unroll
-        for (int nt = 0; nt < kRhsTiles; ++nt) part[slab(t, nt)] = acc[t][nt];
-    }
-    __syncthreads();
-    if (wave < 2) {
-      const f32x4* part = wave == 0 ? part2 : part3;
-#pragma unroll
-      for (int t = 0; t < T; ++t)
-#pragma unroll
-        for (int nt = 0; nt < kRhsTiles; ++nt) acc[t][nt] += part[slab(t, nt)];
-    }
-    __syncthreads();
-    if (wave == 1) {
-#pragma unroll
-      for (int t = 0; t < T; ++t)
-#pragma unroll
-        for (int nt = 0; nt < kRhsTiles; ++nt) part2[slab(t, nt)] = acc[t][nt];
-    }
-    __syncthreads();
-    if (wave != 0) return;
-#pragma unroll
-    for (int t = 0; t < T; ++t)
-#pragma unroll
-      for (int nt = 0; nt < kRhsTiles; ++nt) acc[t][nt] += part2[slab(t, nt)];
-  }
+  // A shared row's partial slabs are summed into wave 0's acc; a packed
+  // row's wave already holds its row's sums.
+  if (shared && !reduce_partials<RHS, T>(acc, lds, wave, lane)) return;
   const int64_t ldc = L.a.scalar_rows;
   if constexpr (kDirect) {
     // Lane x holds rows 4 x .. 4 x + 3 of output columns 4 g + v: one
@@ -417,8 +424,10 @@ __global__ __launch_bounds__(kThreads) void row_owned_mfma_kernel(Launch L) {
   __shared__ __attribute__((aligned(16))) char lds[Lds<RHS>::kTotal];
   const int wave = uniform(int(threadIdx.x) / kWave);
   const int lane = int(threadIdx.x) % kWave;
-  const RowItem item = L.rows[blockIdx.x];
-  if (uniform(item.step_count) < 0) return;  // padding slot: the whole workgroup leaves
+  const WaveItem item = L.items[int64_t(blockIdx.x) * kWaves + wave];
+  // An idle wave leaves.  A workgroup whose row is shared has no idle wave,
+  // so no wave that leaves here is awaited at a barrier.
+  if (uniform(item.step_count) < 0) return;
   switch ((uniform(item.h) + 15) >> 4) {
   case 1: row_body<RHS, 1>(L, item, lds, wave, lane); break;
   case 2: row_body<RHS, 2>(L, item, lds, wave, lane); break;
@@ -454,7 +463,7 @@ void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& s, con
   if (s.groups <= 0) return;
   if (s.groups > int64_t(0x7fffffff)) throw std::invalid_argument("schedule too large for one launch");
   const void* rows = rhs >= 32 && s.rows_wide != nullptr ? s.rows_wide : s.rows;
-  const Launch L{a, static_cast<const StepRec*>(s.steps), static_cast<const RowItem*>(rows), s.step_limit, b, c};
+  const Launch L{a, static_cast<const StepRec*>(s.steps), static_cast<const WaveItem*>(rows), s.step_limit, b, c};
   switch (rhs) {
   case 8: launch<8>(L, s.groups, stream); break;
   case 16: launch<16>(L, s.groups, stream); break;

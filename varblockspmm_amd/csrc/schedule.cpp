@@ -8,7 +8,9 @@
 //    of width 8 mod 16) holds where the step's A columns and B rows start, so
 //    the kernel never walks block metadata: a wave loads the records of all
 //    its steps of a row with one load;
-//  * one workgroup owns one block row;
+//  * one workgroup owns one block row, or up to four light rows (at most
+//    kPackSteps k steps each), one per wave, so that rows too short to keep
+//    four waves busy do not leave three of them idle;
 //  * workgroups are dispatched to the 8 XCDs round-robin by index, so each
 //    XCD's rows (its band) are placed at indices x, x + 8, x + 16, ...;
 //  * a block row goes to the XCD whose eighth of the block columns holds the
@@ -55,102 +57,135 @@ HostSchedule build_schedule(const vbsr_host_view& m) {
     if (out.steps.size() > size_t(INT32_MAX)) throw std::invalid_argument("too many k steps for one matrix");
     step_first[size_t(i) + 1] = int32_t(out.steps.size());
   }
+  auto steps_of = [&](int32_t i) { return step_first[size_t(i) + 1] - step_first[size_t(i)]; };
 
-  // Cost of a row: its 16-row tiles times its k steps, plus a fixed per-row
-  // overhead (in units of one 16 x 16 x 16 MFMA step).
-  std::vector<int64_t> work(static_cast<size_t>(rows));
-  for (int32_t i = 0; i < rows; ++i)
-    work[size_t(i)] = int64_t((m.row_size[i] + 15) / 16) * (step_first[size_t(i) + 1] - step_first[size_t(i)]) + 8;
+  // Cost of a row: its 16-row tiles times its k steps (in units of one
+  // 16 x 16 x 16 MFMA step).
+  std::vector<int64_t> row_work(static_cast<size_t>(rows));
+  for (int32_t i = 0; i < rows; ++i) row_work[size_t(i)] = int64_t((m.row_size[i] + 15) / 16) * steps_of(i);
 
-  // Home eighth of each row: the eighth of the block columns holding the
-  // largest share of its block widths.
-  const int32_t cols = m.block_cols;
-  std::vector<std::array<int64_t, kXcds>> share(static_cast<size_t>(rows));
+  // Workgroups ("units"): every row of more than kPackSteps steps alone;
+  // the light rows, heaviest first, kRowWaves at a time.  A unit's cost is
+  // its rows' work plus a fixed per-workgroup overhead.
+  std::vector<std::vector<int32_t>> units;
+  std::vector<int32_t> light;
   for (int32_t i = 0; i < rows; ++i) {
-    share[size_t(i)].fill(0);
-    for (int32_t blk = m.row_ptr[i]; blk < m.row_ptr[i + 1]; ++blk) {
-      const int32_t c = m.block_col[blk];
-      share[size_t(i)][size_t(std::min<int64_t>(kXcds - 1, int64_t(c) * kXcds / cols))] += m.col_size[c];
-    }
+    if (steps_of(i) > kPackSteps)
+      units.push_back({i});
+    else
+      light.push_back(i);
   }
-  auto top_share = [&](int32_t i) { return *std::max_element(share[size_t(i)].begin(), share[size_t(i)].end()); };
-  std::vector<int32_t> order(static_cast<size_t>(rows));
-  std::iota(order.begin(), order.end(), 0);
-  std::stable_sort(order.begin(), order.end(), [&](int32_t x, int32_t y) { return top_share(x) > top_share(y); });
+  std::stable_sort(light.begin(), light.end(),
+                   [&](int32_t x, int32_t y) { return row_work[size_t(x)] > row_work[size_t(y)]; });
+  for (size_t q = 0; q < light.size(); q += kRowWaves)
+    units.emplace_back(light.begin() + std::ptrdiff_t(q),
+                       light.begin() + std::ptrdiff_t(std::min(light.size(), q + size_t(kRowWaves))));
+  const size_t n_units = units.size();
+  std::vector<int64_t> work(n_units, 8);
+  for (size_t u = 0; u < n_units; ++u)
+    for (const int32_t i : units[u]) work[u] += row_work[size_t(i)];
+
+  // Home eighth of each unit: the eighth of the block columns holding the
+  // largest share of its rows' block widths.
+  const int32_t cols = m.block_cols;
+  std::vector<std::array<int64_t, kXcds>> share(n_units);
+  for (size_t u = 0; u < n_units; ++u) {
+    share[u].fill(0);
+    for (const int32_t i : units[u])
+      for (int32_t blk = m.row_ptr[i]; blk < m.row_ptr[i + 1]; ++blk) {
+        const int32_t c = m.block_col[blk];
+        share[u][size_t(std::min<int64_t>(kXcds - 1, int64_t(c) * kXcds / cols))] += m.col_size[c];
+      }
+  }
+  auto top_share = [&](size_t u) { return *std::max_element(share[u].begin(), share[u].end()); };
+  std::vector<size_t> order(n_units);
+  std::iota(order.begin(), order.end(), size_t(0));
+  std::stable_sort(order.begin(), order.end(), [&](size_t x, size_t y) { return top_share(x) > top_share(y); });
 
   const int64_t total = std::accumulate(work.begin(), work.end(), int64_t(0));
   const int64_t cap = total / kXcds + 1;
   std::array<int64_t, kXcds> load{};
-  std::vector<std::vector<int32_t>> bands(kXcds);
-  for (const int32_t i : order) {
+  std::vector<std::vector<size_t>> bands(kXcds);
+  for (const size_t u : order) {
     std::array<int, kXcds> rank{};
     std::iota(rank.begin(), rank.end(), 0);
-    std::stable_sort(rank.begin(), rank.end(),
-                     [&](int x, int y) { return share[size_t(i)][size_t(x)] > share[size_t(i)][size_t(y)]; });
+    std::stable_sort(rank.begin(), rank.end(), [&](int x, int y) { return share[u][size_t(x)] > share[u][size_t(y)]; });
     int chosen = -1;
     for (const int x : rank)
-      if (load[size_t(x)] + work[size_t(i)] <= cap) {
+      if (load[size_t(x)] + work[u] <= cap) {
         chosen = x;
         break;
       }
     if (chosen < 0) chosen = int(std::min_element(load.begin(), load.end()) - load.begin());
-    bands[size_t(chosen)].push_back(i);
-    load[size_t(chosen)] += work[size_t(i)];
+    bands[size_t(chosen)].push_back(u);
+    load[size_t(chosen)] += work[u];
   }
 
   int64_t per_xcd = 0;
   for (auto& band : bands) {
-    std::stable_sort(band.begin(), band.end(), [&](int32_t x, int32_t y) { return work[size_t(x)] > work[size_t(y)]; });
+    std::stable_sort(band.begin(), band.end(), [&](size_t x, size_t y) { return work[x] > work[y]; });
     per_xcd = std::max<int64_t>(per_xcd, int64_t(band.size()));
   }
   out.groups = per_xcd * kXcds;
 
-  // Lays the bands out in launch order: the row at position pos of XCD x's
-  // band is workgroup pos * 8 + x; missing positions are padding slots.
-  auto emit = [&](const std::vector<std::vector<int32_t>>& ordered, std::vector<RowItem>& items) {
-    RowItem padding{};
-    padding.step_count = -1;
-    padding.row = -1;
-    items.assign(size_t(out.groups), padding);
+  // Lays the bands out in launch order: the unit at position pos of XCD x's
+  // band is workgroup pos * 8 + x; missing positions are padding
+  // workgroups, all of whose waves are idle.
+  auto emit = [&](const std::vector<std::vector<size_t>>& ordered, std::vector<WaveItem>& items) {
+    WaveItem idle{};
+    idle.step_count = -1;
+    idle.row = -1;
+    idle.group = 1;
+    items.assign(size_t(out.groups) * kRowWaves, idle);
     for (int xcd = 0; xcd < kXcds; ++xcd) {
       const auto& band = ordered[size_t(xcd)];
       for (size_t pos = 0; pos < band.size(); ++pos) {
-        const int32_t i = band[pos];
-        RowItem& item = items[pos * kXcds + size_t(xcd)];
-        item.c_off = m.row_scalar_off[i];
-        item.step_first = step_first[size_t(i)];
-        item.step_count = step_first[size_t(i) + 1] - step_first[size_t(i)];
-        item.h = m.row_size[i];
-        item.row = i;
-        for (int w = 0; w < kRowWaves; ++w)
-          if (kStepRun * w < item.step_count) item.first[w] = out.steps[size_t(item.step_first + kStepRun * w)];
+        const auto& unit = units[band[pos]];
+        WaveItem* wg = &items[(pos * kXcds + size_t(xcd)) * kRowWaves];
+        const bool shared = steps_of(unit[0]) > kPackSteps;
+        for (int w = 0; w < kRowWaves; ++w) {
+          if (!shared && size_t(w) >= unit.size()) continue;
+          const int32_t i = shared ? unit[0] : unit[size_t(w)];
+          WaveItem& item = wg[w];
+          item.c_off = m.row_scalar_off[i];
+          item.step_first = step_first[size_t(i)];
+          item.step_count = steps_of(i);
+          item.h = m.row_size[i];
+          item.row = i;
+          item.group = shared ? kRowWaves : 1;
+          item.lead = shared ? w : 0;
+          const int32_t first = shared ? kStepRun * w : 0;
+          if (first < item.step_count) item.first = out.steps[size_t(item.step_first + first)];
+        }
       }
     }
   };
   emit(bands, out.rows);
 
-  // Chained order of each band for RHS 32 and 64.  A row's affinity to the
-  // rows already placed counts 2 per shared block column and 1 per
-  // neighbouring one; the next row is the unplaced one of highest affinity,
-  // ties to the heavier (then earlier) row.  Affinities only grow, so a
+  // Chained order of each band for RHS 32 and 64.  A unit's affinity to the
+  // units already placed counts 2 per shared block column and 1 per
+  // neighbouring one; the next unit is the unplaced one of highest affinity,
+  // ties to the heavier (then earlier) unit.  Affinities only grow, so a
   // max-heap with stale entries skipped finds it.  A block column used by
-  // more than kMaxUsers rows of the band adds no affinity: it says little
-  // about which rows belong together, and skipping it bounds the work by
+  // more than kMaxUsers units of the band adds no affinity: it says little
+  // about which units belong together, and skipping it bounds the work by
   // 3 * kMaxUsers updates per block instead of growing with the square of
-  // the rows that share a column.
+  // the units that share a column.
   constexpr size_t kMaxUsers = 64;
   std::vector<std::vector<int32_t>> users(static_cast<size_t>(cols));
-  std::vector<std::vector<int32_t>> chained(kXcds);
+  std::vector<std::vector<size_t>> chained(kXcds);
   for (int xcd = 0; xcd < kXcds; ++xcd) {
     const auto& band = bands[size_t(xcd)];
     const size_t n = band.size();
-    const size_t head = n - n / 4;  // rows chained; the rest is the light tail
+    const size_t head = n - n / 4;  // units chained; the rest is the light tail
     for (auto& u : users) u.clear();
-    for (size_t q = 0; q < head; ++q)
-      for (int32_t blk = m.row_ptr[band[q]]; blk < m.row_ptr[band[q] + 1]; ++blk)
-        users[size_t(m.block_col[blk])].push_back(int32_t(q));
+    auto for_each_col = [&](size_t unit, auto&& f) {
+      for (const int32_t i : units[unit])
+        for (int32_t blk = m.row_ptr[i]; blk < m.row_ptr[i + 1]; ++blk) f(m.block_col[blk]);
+    };
+    for (size_t q = 0; q < head; ++q) for_each_col(band[q], [&](int32_t c) { users[size_t(c)].push_back(int32_t(q)); });
     // Heap keys: affinity in the high word, then the lower position (the
-    // band is sorted heaviest first, so that is the heavier row).
+    // band is sorted heaviest first, so that is the heavier unit).
     auto key = [](uint64_t affinity, size_t q) { return (affinity << 32) | (0xffffffffu - uint32_t(q)); };
     std::vector<uint32_t> affinity(head, 0), gain(head, 0);
     std::vector<char> placed(head, 0);
@@ -165,11 +200,10 @@ HostSchedule build_schedule(const vbsr_host_view& m) {
       if (placed[q] || (top >> 32) != affinity[q]) continue;  // placed, or a stale entry
       placed[q] = 1;
       order_out.push_back(band[q]);
-      // Gains of the rows this placement touches, summed first so that each
-      // touched row is pushed once.
+      // Gains of the units this placement touches, summed first so that each
+      // touched unit is pushed once.
       touched.clear();
-      for (int32_t blk = m.row_ptr[band[q]]; blk < m.row_ptr[band[q] + 1]; ++blk) {
-        const int32_t c = m.block_col[blk];
+      for_each_col(band[q], [&](int32_t c) {
         for (int32_t d = -1; d <= 1; ++d) {
           if (c + d < 0 || c + d >= cols || users[size_t(c + d)].size() > kMaxUsers) continue;
           for (const int32_t r : users[size_t(c + d)]) {
@@ -178,7 +212,7 @@ HostSchedule build_schedule(const vbsr_host_view& m) {
             gain[size_t(r)] += d == 0 ? 2 : 1;
           }
         }
-      }
+      });
       for (const int32_t r : touched) {
         affinity[size_t(r)] += gain[size_t(r)];
         gain[size_t(r)] = 0;
