@@ -13,6 +13,9 @@
 //    clamp_local_columns (clamped instead of cyclic local columns).
 //  - launch_row_owned takes the matrix's row schedule instead of the
 //    reference's row_shape_order and h <= 16 partition counts.
+//  - Kernel::SplitRow, reserved and rejected in the reference, selects the
+//    split-row path (also reachable as launch_split_row); Kernel::Auto takes
+//    it for few long rows.
 #pragma once
 
 #include <cstdint>
@@ -174,7 +177,9 @@ inline std::vector<float> cpu_reference(const HostMatrix& matrix, const std::vec
   return C;
 }
 
-/** Kernel selection; SplitRow is reserved and rejected (reference vbsr.hpp:91). */
+/** Kernel selection (reference vbsr.hpp:91).  SplitRow, reserved in the
+ * reference, is the split-row path here (two launches, a plan-owned
+ * workspace); Auto takes it for few long rows, else RowOwned. */
 enum class Kernel { Auto, RowOwned, SplitRow };
 
 /** Configuration for a reusable execution plan (reference vbsr.hpp:94-97). */
@@ -262,6 +267,20 @@ private:
 inline void launch_row_owned(DeviceMatrix matrix, const vbsr_row_schedule& schedule, const float* B, float* C,
                              int rhs, hipStream_t stream) {
   detail::check(vbsr_launch_row_owned(&matrix, &schedule, B, C, rhs, stream));
+}
+
+/** Bytes of workspace the split-row path needs for `matrix` at `rhs`. */
+inline int64_t split_row_workspace_bytes(const Matrix& matrix, int rhs) {
+  int64_t bytes = 0;
+  detail::check(vbsr_split_row_workspace_bytes(matrix.handle(), rhs, &bytes));
+  return bytes;
+}
+
+/** The split-row path (the reference's reserved Kernel::SplitRow) with a
+ * caller-owned device workspace of split_row_workspace_bytes(matrix, rhs). */
+inline void launch_split_row(const Matrix& matrix, const float* B, float* C, int rhs, void* workspace,
+                             int64_t workspace_bytes, hipStream_t stream) {
+  detail::check(vbsr_launch_split_row(matrix.handle(), B, C, rhs, workspace, workspace_bytes, stream));
 }
 
 /** The reference-order kernel (reference vbsr.hpp:161). */

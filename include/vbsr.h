@@ -162,15 +162,24 @@ typedef struct vbsr_row_schedule {
 int vbsr_matrix_row_schedule(const vbsr_matrix* matrix, vbsr_row_schedule* out);
 
 /* Plan(const Matrix&, PlanOptions) (vbsr.hpp:106; plan.cpp:5-18): rejects
- * rhs_width outside {8,16,32,64} and VBSR_KERNEL_SPLIT_ROW.  The plan views
- * the matrix, which must outlive it. */
+ * rhs_width outside {8,16,32,64}.  VBSR_KERNEL_ROW_OWNED runs the row-owned
+ * kernel; VBSR_KERNEL_SPLIT_ROW (reserved and rejected in the reference,
+ * plan.cpp:13-17) runs the split-row path (vbsr_launch_split_row) with a
+ * workspace the plan allocates here and frees when destroyed;
+ * VBSR_KERNEL_AUTO takes the split-row path for matrices whose row-owned
+ * launch would leave most CUs idle while their rows are long (few block rows
+ * of high degree), else the row-owned kernel.  The plan views the matrix,
+ * which must outlive it. */
 int vbsr_plan_create(const vbsr_matrix* matrix, const vbsr_plan_options* options, vbsr_plan** out);
 void vbsr_plan_destroy(vbsr_plan* plan);
 /* Plan::execute (vbsr.hpp:110; plan.cpp:19-22): enqueues C = A * B on
- * `stream` (0 = null stream). */
+ * `stream` (0 = null stream).  Allocates nothing, also on the split-row
+ * path; a split-row plan's executes share its workspace, so one plan must
+ * not execute on two streams at once. */
 int vbsr_plan_execute(const vbsr_plan* plan, const float* B, float* C, hipStream_t stream);
 /* Plan::launch_count (vbsr.hpp:112; plan.cpp:23-31): kernels enqueued by one
- * vbsr_plan_execute. */
+ * vbsr_plan_execute: 2 on the split-row path, else 1 (0 for a matrix
+ * without block rows). */
 int vbsr_plan_launch_count(const vbsr_plan* plan);
 
 /* launch_row_owned (vbsr.hpp:158-159; row_owned.cu:397-423): the tuned
@@ -182,6 +191,21 @@ int vbsr_plan_launch_count(const vbsr_plan* plan);
  * vbsr_plan_execute takes any K). */
 int vbsr_launch_row_owned(const vbsr_device_view* matrix, const vbsr_row_schedule* schedule,
                           const float* B, float* C, int32_t rhs, hipStream_t stream);
+
+/* The split-row path (the reference's reserved Kernel::SplitRow,
+ * vbsr.hpp:91, plan.cpp:13-17).  Each block row's k steps are cut into parts
+ * (the matrix's split schedule, built at vbsr_matrix_create); the row-owned
+ * kernel computes each part's partial slab into `workspace`, and a second
+ * launch sums each row's partial slabs into C in part order.  Results are
+ * bit-identical from run to run (fixed order, no atomics) and within the
+ * row-owned kernel's tolerance of cpu_reference.  `workspace` is a device
+ * buffer of at least vbsr_split_row_workspace_bytes(matrix, rhs) bytes,
+ * 4-byte aligned, overlapping neither B nor C, that no other launch uses
+ * until this one has finished.  K is bounded as for vbsr_launch_row_owned.
+ * Two launches; allocates nothing. */
+int vbsr_split_row_workspace_bytes(const vbsr_matrix* matrix, int32_t rhs, int64_t* bytes);
+int vbsr_launch_split_row(const vbsr_matrix* matrix, const float* B, float* C, int32_t rhs, void* workspace,
+                          int64_t workspace_bytes, hipStream_t stream);
 
 /* launch_row_owned_scalar (vbsr.hpp:161; row_owned.cu:376-395): one output
  * per lane, accumulated with fmaf over blocks in row_ptr order and k

@@ -104,7 +104,11 @@ void run_negative_tests() {
   expect_invalid_argument([&] { vbsr::Matrix m(bad); }, "Matrix accepted an invalid host matrix");
   vbsr::Matrix device(valid);
   expect_invalid_argument([&] { vbsr::Plan plan(device, {7, vbsr::Kernel::RowOwned}); }, "invalid RHS accepted");
-  expect_invalid_argument([&] { vbsr::Plan plan(device, {8, vbsr::Kernel::SplitRow}); }, "split-row accepted");
+  // Kernel::SplitRow, reserved and rejected in the reference (test_main.cpp:140), is the split-row path here;
+  // kernels outside the enumeration are still rejected.
+  if (vbsr::Plan(device, {8, vbsr::Kernel::SplitRow}).launch_count() != 2)
+    throw std::runtime_error("split-row plan should take two launches");
+  expect_invalid_argument([&] { vbsr::Plan plan(device, {8, static_cast<vbsr::Kernel>(3)}); }, "kernel 3 accepted");
   expect_invalid_argument([&] { vbsr::ScalarCsrPlan plan(valid, 12); }, "CSR plan accepted an invalid RHS");
   expect_invalid_argument([&] { vbsr::ScalarCsrPlan plan(bad, 8); }, "CSR plan accepted an invalid host matrix");
   expect_invalid_argument([&] { vbsr::GroupedGemmPlan plan(valid, 24); }, "grouped plan accepted an invalid RHS");
@@ -152,6 +156,11 @@ void run_case(vbsr::Distribution distribution, int degree, int rhs, bool local, 
 
   const std::string tag = " (degree " + std::to_string(degree) + ", rhs " + std::to_string(rhs) + ", seed " +
                           std::to_string(seed) + ")";
+  vbsr::Plan split(device, {rhs, vbsr::Kernel::SplitRow});
+  c.poison();
+  split.execute(b.ptr, c.ptr, stream);
+  hip_ok(hipStreamSynchronize(stream), "sync");
+  compare(c.read(), reference, bound, "split-row" + tag);
   vbsr::Plan plan(device, {rhs, vbsr::Kernel::RowOwned});
   if (plan.launch_count() != 1) throw std::runtime_error("launch_count != 1" + tag);
   c.poison();

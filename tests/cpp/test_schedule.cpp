@@ -11,6 +11,9 @@
 //     no XCD's work exceeds an eighth of the total by more than one row's;
 //   * `rows` runs each XCD's workgroups heaviest first; `rows_wide` ends each
 //     XCD's band with its lightest quarter, heaviest first;
+//   * the split-row schedule: each row's parts cover its steps in order and
+//     take consecutive virtual rows, every part is in exactly one workgroup,
+//     and the automatic choice follows its rule;
 //   * building twice gives the same schedule;
 //   * matrices whose rows share few block columns (every row on the same 8
 //     columns; rows overlapping in 15 of 16 columns) build in seconds: the
@@ -23,6 +26,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <vector>
 
 #include "internal.hpp"
@@ -159,6 +163,81 @@ void check_steps(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s) {
   CHECK(int64_t(s.steps.size()) == expected_first);
 }
 
+// The split-row schedule: every row has at least one part; a row's parts
+// take consecutive virtual rows (part q at w_off + q * h) and, in order, its
+// consecutive steps, each part at most part_steps long; the workgroups hold
+// every part once (a part of more than kPackSteps steps shared by all waves,
+// shorter ones packed one per wave, idle waves last); the automatic choice
+// follows its rule.
+void check_split(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s) {
+  using vbsr_amd::kPackSteps;
+  using vbsr_amd::kRowWaves;
+  const auto& sp = s.split;
+  CHECK(int64_t(sp.rows.size()) == m.block_rows);
+  CHECK(sp.part_steps > 0 && sp.part_steps % (kRowWaves * vbsr_amd::kStepRun) == 0);
+  CHECK(int64_t(sp.items.size()) == sp.groups * kRowWaves && sp.groups % vbsr_amd::kXcds == 0);
+  // step_first of each row from the row items (the lead wave of each row)
+  std::vector<int32_t> row_first(size_t(m.block_rows), -1), row_count(size_t(m.block_rows), -1);
+  for (const auto& item : s.rows)
+    if (item.step_count >= 0 && item.lead == 0) {
+      row_first[size_t(item.row)] = item.step_first;
+      row_count[size_t(item.row)] = item.step_count;
+    }
+  int64_t virtual_rows = 0;
+  std::map<int64_t, const vbsr_amd::WaveItem*> by_offset;  // a part's first virtual row -> its item
+  for (int64_t g = 0; g < sp.groups; ++g) {
+    const auto* wg = &sp.items[size_t(g) * kRowWaves];
+    const bool shared = wg[0].step_count >= 0 && wg[0].group == kRowWaves;
+    bool idle_seen = false;
+    for (int w = 0; w < kRowWaves; ++w) {
+      const auto& item = wg[w];
+      if (item.step_count < 0) {
+        CHECK(!shared);
+        idle_seen = true;
+        continue;
+      }
+      CHECK(!idle_seen);
+      if (shared) {
+        CHECK(item.group == kRowWaves && item.lead == w && item.c_off == wg[0].c_off);
+        CHECK(item.step_count > kPackSteps);
+      } else {
+        CHECK(item.group == 1 && item.lead == 0 && item.step_count <= kPackSteps);
+      }
+      const int32_t first = shared ? item.step_first + vbsr_amd::kStepRun * w : item.step_first;
+      const bool has = first < item.step_first + item.step_count;
+      CHECK(item.first.a_off == (has ? s.steps[size_t(first)].a_off : 0));
+      CHECK(item.first.b_off == (has ? s.steps[size_t(first)].b_off : 0));
+      if (!shared || w == 0) CHECK(by_offset.emplace(item.c_off, &item).second);
+    }
+  }
+  for (int32_t i = 0; i < m.block_rows; ++i) {
+    const auto& rec = sp.rows[size_t(i)];
+    CHECK(rec.row == i && rec.h == m.row_size[i] && rec.c_off == m.row_scalar_off[i]);
+    CHECK(rec.parts >= 1 && rec.w_off == virtual_rows);
+    int32_t next = row_first[size_t(i)];
+    for (int32_t q = 0; q < rec.parts; ++q) {
+      const auto it = by_offset.find(rec.w_off + int64_t(q) * rec.h);
+      CHECK(it != by_offset.end());
+      const auto& item = *it->second;
+      CHECK(item.row == i && item.h == rec.h && item.step_first == next);
+      CHECK(item.step_count <= sp.part_steps && (item.step_count > 0 || rec.parts == 1));
+      next += item.step_count;
+    }
+    CHECK(next == row_first[size_t(i)] + row_count[size_t(i)]);
+    virtual_rows += int64_t(rec.parts) * rec.h;
+  }
+  CHECK(sp.virtual_rows == virtual_rows);
+  int64_t parts = 0;
+  for (const auto& rec : sp.rows) parts += rec.parts;
+  CHECK(int64_t(by_offset.size()) == parts);
+  int32_t longest = 0;
+  int64_t units = 0;
+  for (int64_t g = 0; g < s.groups; ++g)
+    if (s.rows[size_t(g) * kRowWaves].step_count >= 0) ++units;
+  for (int32_t i = 0; i < m.block_rows; ++i) longest = std::max(longest, row_count[size_t(i)]);
+  CHECK(s.split_preferred == (units < 160 && longest > 2 * kRowWaves * vbsr_amd::kStepRun));
+}
+
 bool same(const std::vector<vbsr_amd::WaveItem>& a, const std::vector<vbsr_amd::WaveItem>& b) {
   return a.size() == b.size() && (a.empty() || std::memcmp(a.data(), b.data(), a.size() * sizeof(a[0])) == 0);
 }
@@ -173,11 +252,13 @@ void check_view(const vbsr_host_view& m, const char* name, double max_seconds) {
     ++failures;
   }
   check_steps(m, s);
+  check_split(m, s);
   std::vector<int> xcd_of_row(size_t(m.block_rows), -1);
   check_order(m, s, s.rows, xcd_of_row, false);
   check_order(m, s, s.rows_wide, xcd_of_row, true);
   const vbsr_amd::HostSchedule again = vbsr_amd::build_schedule(m);
-  if (!(same(s.rows, again.rows) && same(s.rows_wide, again.rows_wide) && s.steps.size() == again.steps.size())) {
+  if (!(same(s.rows, again.rows) && same(s.rows_wide, again.rows_wide) && same(s.split.items, again.split.items) &&
+        s.steps.size() == again.steps.size())) {
     std::fprintf(stderr, "FAILED: schedule not deterministic\n");
     ++failures;
   }

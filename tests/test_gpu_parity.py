@@ -400,6 +400,98 @@ def test_order_preserving_kernel_gives_the_closed_form_bits(probe):
     c.close()
 
 
+# ---- the split-row path (the reference's reserved Kernel::SplitRow) -----------------------------
+
+
+@pytest.mark.parametrize("case", reference_cases(), ids=lambda c: "{}-d{}-n{}-{}-s{}".format(*c))
+def test_split_row_reference_parameter_matrix(case):
+    """Kernel::SplitRow on the reference test's parameter matrix: within tolerance of the oracle,
+    bit-identical across runs, two launches."""
+    distribution, degree, rhs, locality, seed = case
+    note(f"split-row case {case}")
+    c = Case(vb.generate(9, 17, degree, distribution, locality, seed), rhs, seed)
+    plan = vb.Plan(c.matrix, rhs, "split_row")
+    assert plan.launch_count() == 2
+    first = c.run_plan(plan)
+    c.check_tolerance(first, "split-row")
+    np.testing.assert_array_equal(c.run_plan(plan), first, err_msg="split-row not bit-identical across runs")
+    plan.close()
+    c.close()
+
+
+SPLIT_CASES = [
+    # (name, rows, degree, distribution, locality, rhs, seed, auto takes the split-row path)
+    ("few-rows-32-n8", 32, 16, "high", "random", 8, 1, True),
+    ("few-rows-32-n64", 32, 16, "high", "random", 64, 1, True),
+    ("few-rows-128-n32", 128, 16, "high", "random", 32, 1, True),
+    ("few-rows-256-n32", 256, 16, "high", "random", 32, 1, False),
+    ("few-rows-64-d4", 64, 4, "high", "random", 16, 2, False),
+    ("config3-n32", 4096, 8, "high", "random", 32, 1, False),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: c[0])
+def test_split_row_against_oracle_and_auto_choice(case):
+    """Kernel::SplitRow at few rows (where Auto takes it) and at configuration 3 (where Auto does not):
+    within tolerance of the oracle and bit-stable; Auto's plan takes the expected path and gives the
+    same bits as the explicit plan of that path."""
+    name, rows, degree, distribution, locality, rhs, seed, auto_split = case
+    note(f"split-row {name}")
+    c = Case(vb.generate(rows, rows, degree, distribution, locality, seed), rhs, seed)
+    split = vb.Plan(c.matrix, rhs, "split_row")
+    first = c.run_plan(split)
+    c.check_tolerance(first, name)
+    np.testing.assert_array_equal(c.run_plan(split), first)
+    auto = vb.Plan(c.matrix, rhs, "auto")
+    assert auto.launch_count() == (2 if auto_split else 1)
+    expected = first if auto_split else c.run_plan(vb.Plan(c.matrix, rhs, "row_owned"))
+    np.testing.assert_array_equal(c.run_plan(auto), expected)
+    split.close()
+    auto.close()
+    c.close()
+
+
+@pytest.mark.parametrize("name", ["empty-repeat-unsorted", "all-empty", "single-row", "long-row", "packed-light"])
+def test_split_row_edge_matrices(name):
+    """Empty rows (a zero-step part each), a row of 400 steps (parts beyond one workgroup segment),
+    packed parts of every height."""
+    note(f"split-row edge {name}")
+    host = EDGE_MATRICES[name]()
+    for rhs in (8, 64):
+        c = Case(host, rhs, 19)
+        c.check_tolerance(c.run_plan(vb.Plan(c.matrix, rhs, "split_row")), f"split-row {name} rhs={rhs}")
+        c.close()
+
+
+def test_launch_split_row_with_a_caller_workspace():
+    """vbsr_launch_split_row: a caller's workspace of the reported size gives the split-row plan's bits;
+    a smaller one, a misaligned one, or one overlapping B or C is refused before any launch."""
+    note("launch_split_row")
+    rhs = 32
+    c = Case(vb.generate(48, 48, 16, "high", "random", 4), rhs, 4)
+    expected = c.run_plan(vb.Plan(c.matrix, rhs, "split_row"))
+    nbytes = vb.split_row_workspace_bytes(c.matrix, rhs)
+    # The split schedule's rule: parts of 8 steps here (1,184 steps, far below 8 x 2048), at least one per row;
+    # one partial slab (h x rhs floats) per part.
+    widths = c.host.col_size[c.host.block_col]
+    steps = np.add.reduceat(widths // 16 + (widths % 16 != 0), c.host.row_ptr[:-1])
+    parts = np.maximum(1, -(-steps // 8))
+    assert nbytes == 4 * rhs * int(np.sum(parts * c.host.row_size))
+    workspace = torch.empty(nbytes // 4 + 16, dtype=torch.float32, device=DEVICE)
+    result = c.run(lambda: vb.launch_split_row(c.matrix, c.b_dev, c.c_dev, rhs, workspace, nbytes, c.stream))
+    np.testing.assert_array_equal(result, expected)
+    with pytest.raises(ValueError, match="too small"):
+        vb.launch_split_row(c.matrix, c.b_dev, c.c_dev, rhs, workspace, nbytes - 4, c.stream)
+    with pytest.raises(ValueError, match="aligned"):
+        vb.launch_split_row(c.matrix, c.b_dev, c.c_dev, rhs, workspace.data_ptr() + 2, nbytes, c.stream)
+    with pytest.raises(ValueError, match="overlap"):
+        vb.launch_split_row(c.matrix, c.b_dev, c.c_dev, rhs, c.c_dev, nbytes, c.stream)
+    with pytest.raises(ValueError):
+        vb.launch_split_row(c.matrix, c.b_dev, c.c_dev, rhs, None, nbytes, c.stream)
+    torch.cuda.synchronize()
+    c.close()
+
+
 def test_device_matrix_errors():
     note("device errors")
     host = vb.generate(6, 6, 2, "high", "random", 1)
@@ -416,8 +508,10 @@ def test_device_matrix_errors():
     for rhs in (0, 7, 33, 128):
         with pytest.raises(ValueError):
             vb.Plan(m, rhs)
-    with pytest.raises(ValueError):
-        vb.Plan(m, 8, "split_row")
+    for kernel in (3, -1):
+        with pytest.raises(ValueError):
+            vb.Plan(m, 8, kernel)
+    assert vb.Plan(m, 8, "split_row").launch_count() == 2
     plan = vb.Plan(m, 32, "auto")
     assert plan.launch_count() == 1
     b = torch.zeros(m.scalar_cols * 32, device=DEVICE)

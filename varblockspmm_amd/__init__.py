@@ -86,6 +86,8 @@ SIGNATURES = {
     "vbsr_launch_row_owned": (ctypes.c_int, [ctypes.POINTER(DeviceView), ctypes.POINTER(RowSchedule), _P, _P,
                                              ctypes.c_int32, _P]),
     "vbsr_launch_row_owned_scalar": (ctypes.c_int, [ctypes.POINTER(DeviceView), _P, _P, ctypes.c_int32, _P]),
+    "vbsr_split_row_workspace_bytes": (ctypes.c_int, [_P, ctypes.c_int32, ctypes.POINTER(ctypes.c_int64)]),
+    "vbsr_launch_split_row": (ctypes.c_int, [_P, _P, _P, ctypes.c_int32, _P, ctypes.c_int64, _P]),
     "vbsr_csr_plan_create": (ctypes.c_int, [ctypes.POINTER(HostView), ctypes.c_int32, ctypes.POINTER(_P)]),
     "vbsr_csr_plan_destroy": (None, [_P]),
     "vbsr_csr_plan_execute": (ctypes.c_int, [_P, _P, _P, _P]),
@@ -333,6 +335,24 @@ def launch_row_owned_scalar(device_view, B, C, rhs, stream=None):
     _check_panel(C, device_view.scalar_rows * int(rhs), "C")
     _check(library().vbsr_launch_row_owned_scalar(ctypes.byref(device_view), _address(B), _address(C), int(rhs),
                                                   _stream(stream)))
+
+
+def split_row_workspace_bytes(matrix, rhs):
+    """Bytes of device workspace the split-row path needs for `matrix` at `rhs`."""
+    out = ctypes.c_int64()
+    _check(library().vbsr_split_row_workspace_bytes(matrix._handle, int(rhs), ctypes.byref(out)))
+    return out.value
+
+
+def launch_split_row(matrix, B, C, rhs, workspace, workspace_bytes=None, stream=None):
+    """The split-row path (the reference's reserved Kernel::SplitRow) with a caller-owned workspace: partial slabs
+    of each row's parts into `workspace`, then their fixed-order sum into C.  Two launches."""
+    _check_panel(B, matrix.scalar_cols * int(rhs), "B")
+    _check_panel(C, matrix.scalar_rows * int(rhs), "C")
+    if workspace_bytes is None:
+        workspace_bytes = workspace.numel() * workspace.element_size() if hasattr(workspace, "numel") else 0
+    _check(library().vbsr_launch_split_row(matrix._handle, _address(B), _address(C), int(rhs), _address(workspace),
+                                           int(workspace_bytes), _stream(stream)))
 
 
 class ScalarCsrPlan:

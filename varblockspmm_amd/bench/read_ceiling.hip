@@ -7,9 +7,10 @@
 //   dram      1 GiB read once per launch; a second 1 GiB buffer is read
 //             between launches, so nothing of the first is cached in L2 or
 //             in the 256 MB Infinity Cache (MALL).
-//   mall      96 MiB read once per launch, after a warm-up launch: each XCD
-//             streams its eighth (12 MiB, three times its 4 MiB L2) in order,
-//             so every access misses L2 and the Infinity Cache serves it.
+//   mall      96 MiB read 4 times per launch, after a warm-up launch: each
+//             XCD streams its eighth (12 MiB, three times its 4 MiB L2) in
+//             order, so every access misses L2 and the Infinity Cache serves
+//             it.
 //   l2        16 MiB read 8 times per launch: each XCD's eighth (2 MiB) stays
 //             in its L2.
 // Each case runs with plain and with non-temporal 16-byte loads.
@@ -130,7 +131,7 @@ int main(int argc, char** argv) {
     int passes;
     bool flushed;
   };
-  const Case cases[] = {{"dram", GiB, 1, true}, {"mall", 96 * MiB, 1, false}, {"l2", 16 * MiB, 8, false}};
+  const Case cases[] = {{"dram", GiB, 1, true}, {"mall", 96 * MiB, 4, false}, {"l2", 16 * MiB, 8, false}};
   for (const Case& c : cases) {
     for (const bool nt : {false, true}) {
       const Result r = nt ? run<true>(dram, c.bytes, c.passes, c.flushed ? flush : nullptr, GiB, reps, grid, sink,

@@ -24,7 +24,8 @@
 // asks for the reference test's uniform [-1, 1] stream.
 //
 // Methods: row_owned_hybrid (Plan::execute with Kernel::RowOwned, the
-// reference's tuned path), row_owned_scalar (launch_row_owned_scalar) and
+// reference's tuned path; --kernel auto or split_row plans with those
+// kernels instead), row_owned_scalar (launch_row_owned_scalar) and
 // scalar_csr_rocsparse (ScalarCsrPlan, the counterpart of the reference's
 // scalar_csr_cusparse row) and slot_grouped_rocblas (GroupedGemmPlan, the
 // counterpart of slot_grouped_cublas).
@@ -60,6 +61,7 @@ struct Arguments {
   std::string locality = "local";
   std::string distribution = "high";
   std::string input = "constant";
+  std::string kernel = "row_owned";
   bool cold = true;
   bool header = true;
 };
@@ -84,7 +86,8 @@ void usage() {
   std::cerr << "usage: vbsr_benchmark [--rows N] [--degree D] [--rhs 8|16|32|64] [--reps N] [--warmup N]\n"
                "                      [--seed S] [--locality local|random|clamped]\n"
                "                      [--distribution uniform|low|high|bimodal|bimodal8or64|tied8to64]\n"
-               "                      [--input constant|random] [--no-cold] [--no-header]\n";
+               "                      [--input constant|random] [--kernel row_owned|auto|split_row]\n"
+               "                      [--no-cold] [--no-header]\n";
 }
 
 Arguments parse_arguments(int argc, char** argv) {
@@ -104,6 +107,7 @@ Arguments parse_arguments(int argc, char** argv) {
     else if (option == "--locality") a.locality = value();
     else if (option == "--distribution") a.distribution = value();
     else if (option == "--input") a.input = value();
+    else if (option == "--kernel") a.kernel = value();
     else if (option == "--no-cold") a.cold = false;
     else if (option == "--no-header") a.header = false;
     else if (option == "--help") { usage(); std::exit(0); }
@@ -113,6 +117,8 @@ Arguments parse_arguments(int argc, char** argv) {
   if (a.locality != "local" && a.locality != "random" && a.locality != "clamped")
     throw std::runtime_error("unknown locality: " + a.locality);
   if (a.input != "constant" && a.input != "random") throw std::runtime_error("unknown input: " + a.input);
+  if (a.kernel != "row_owned" && a.kernel != "auto" && a.kernel != "split_row")
+    throw std::runtime_error("unknown kernel: " + a.kernel);
   parse_distribution(a.distribution);
   return a;
 }
@@ -253,7 +259,10 @@ int run(const Arguments& a) {
                       8.0 * double(host.block_col.size() + 1);
   const double bytes = 4.0 * sum_hw + 4.0 * double(b_count) + 4.0 * double(c_count) + meta;
 
-  vbsr::Plan plan(matrix, {a.rhs_width, vbsr::Kernel::RowOwned});
+  const vbsr::Kernel kernel = a.kernel == "auto"        ? vbsr::Kernel::Auto
+                              : a.kernel == "split_row" ? vbsr::Kernel::SplitRow
+                                                        : vbsr::Kernel::RowOwned;
+  vbsr::Plan plan(matrix, {a.rhs_width, kernel});
   const vbsr::DeviceMatrix view = matrix.device_view();
   Bench bench;
   if (a.header)
@@ -269,8 +278,11 @@ int run(const Arguments& a) {
               << (t.cold_median > 0 ? bytes / (t.cold_median * 1e6) : 0.0) << ',' << (t.identical ? 1 : 0) << '\n'
               << std::flush;
   };
+  // A split-row plan (two launches) owns the workspace the split-row path needs.
+  const size_t plan_workspace =
+      plan.launch_count() == 2 ? size_t(vbsr::split_row_workspace_bytes(matrix, a.rhs_width)) : 0;
   report("row_owned_hybrid", bench.time([&](hipStream_t s) { plan.execute(b, c, s); }, a, c, c_count),
-         plan.launch_count(), 0);
+         plan.launch_count(), plan_workspace);
   report("row_owned_scalar",
          bench.time([&](hipStream_t s) { vbsr::launch_row_owned_scalar(view, b, c, a.rhs_width, s); }, a, c,
                     c_count),

@@ -170,6 +170,27 @@ int vbsr_launch_row_owned(const vbsr_device_view* matrix, const vbsr_row_schedul
   });
 }
 
+int vbsr_split_row_workspace_bytes(const vbsr_matrix* matrix, int32_t rhs, int64_t* bytes) {
+  return guarded([&] {
+    require(matrix, "matrix");
+    require(bytes, "bytes");
+    if (!vbsr_amd::supported_rhs(rhs)) throw std::invalid_argument("unsupported rhs width");
+    *bytes = vbsr_amd::split_workspace_floats(matrix->device.split(), rhs) * int64_t(sizeof(float));
+  });
+}
+
+int vbsr_launch_split_row(const vbsr_matrix* matrix, const float* B, float* C, int32_t rhs, void* workspace,
+                          int64_t workspace_bytes, hipStream_t stream) {
+  return guarded([&] {
+    require(matrix, "matrix");
+    if (workspace_bytes < 0) throw std::invalid_argument("negative workspace size");
+    if (reinterpret_cast<uintptr_t>(workspace) % alignof(float) != 0)
+      throw std::invalid_argument("workspace must be 4-byte aligned");
+    vbsr_amd::launch_split_row(matrix->device.view(), matrix->device.schedule(), matrix->device.split(), B, C, rhs,
+                               static_cast<float*>(workspace), workspace_bytes / int64_t(sizeof(float)), stream);
+  });
+}
+
 int vbsr_launch_row_owned_scalar(const vbsr_device_view* matrix, const float* B, float* C, int32_t rhs,
                                  hipStream_t stream) {
   return guarded([&] {

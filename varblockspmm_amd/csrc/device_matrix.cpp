@@ -2,7 +2,8 @@
 // (src/format/vbsr.cpp:84-166).  Arrays are copied verbatim (same packed
 // column-major block payload, same 64-bit scalar/value offsets), so the
 // device view has exactly the reference DeviceMatrix semantics.  The only
-// plan-private arrays are the row schedule (schedule.cpp).
+// plan-private arrays are the row schedule and the split-row schedule
+// (schedule.cpp).
 #include <algorithm>
 
 #include <hip/hip_runtime_api.h>
@@ -59,6 +60,11 @@ DeviceMatrix::DeviceMatrix(const vbsr_host_view& host) {
     schedule_.rows_wide = upload(schedule.rows_wide.data(), int64_t(schedule.rows_wide.size()), allocations_);
     schedule_.groups = schedule.groups;
     schedule_.step_limit = int32_t(std::max<size_t>(schedule.steps.size(), 1) - 1);
+    split_.items = upload(schedule.split.items.data(), int64_t(schedule.split.items.size()), allocations_);
+    split_.rows = upload(schedule.split.rows.data(), int64_t(schedule.split.rows.size()), allocations_);
+    split_.groups = schedule.split.groups;
+    split_.virtual_rows = schedule.split.virtual_rows;
+    split_.preferred = schedule.split_preferred;
   } catch (...) {
     release();
     throw;
@@ -70,6 +76,7 @@ void DeviceMatrix::release() noexcept {
   allocations_.clear();
   view_ = vbsr_device_view{};
   schedule_ = vbsr_row_schedule{};
+  split_ = Split{};
 }
 
 DeviceMatrix::~DeviceMatrix() { release(); }

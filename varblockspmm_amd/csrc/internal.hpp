@@ -84,11 +84,38 @@ struct alignas(16) WaveItem {
 };
 static_assert(sizeof(WaveItem) == 48, "WaveItem is read as 12 dwords");
 
+// The split-row path (SplitRow): each block row's k steps are cut into parts
+// of at most `part_steps` steps; the row-owned kernel computes each part's
+// h x RHS partial slab into a workspace of `virtual_rows` rows (part p of a
+// row at virtual rows w_off + p * h), and a second kernel sums each row's
+// slabs into C in part order.
+struct alignas(16) SplitRowRec {
+  int64_t c_off;  // row_scalar_off[row]
+  int64_t w_off;  // the row's first virtual row
+  int32_t h;      // row_size[row]
+  int32_t parts;  // at least 1
+  int32_t row;
+  int32_t pad;
+};
+static_assert(sizeof(SplitRowRec) == 32, "SplitRowRec is read as 8 dwords");
+
+struct HostSplitSchedule {
+  std::vector<WaveItem> items;     // kRowWaves per workgroup; a part's c_off is its first virtual row
+  std::vector<SplitRowRec> rows;   // one per block row
+  int64_t groups{};                // workgroups of the partial launch (multiple of kXcds)
+  int64_t virtual_rows{};          // workspace rows: the sum over parts of h
+  int32_t part_steps{};
+};
+
 struct HostSchedule {
   std::vector<StepRec> steps;       // row after row, blocks in row_ptr order
   std::vector<WaveItem> rows;       // kRowWaves per workgroup, launch order for RHS 8 and 16
   std::vector<WaveItem> rows_wide;  // the same workgroups, launch order for RHS 32 and 64
   int64_t groups{};                 // workgroups of one launch (multiple of kXcds)
+  HostSplitSchedule split;
+  // Whether Plan's automatic choice takes the split-row path: the row-owned
+  // launch would leave most CUs idle while its rows are long.
+  bool split_preferred{};
 };
 
 // Step records plus two launch orders of the workgroups.  Rows of at most
@@ -112,12 +139,23 @@ public:
   DeviceMatrix(const DeviceMatrix&) = delete;
   DeviceMatrix& operator=(const DeviceMatrix&) = delete;
 
+  // Device copy of the split-row schedule.
+  struct Split {
+    const WaveItem* items{};
+    const SplitRowRec* rows{};
+    int64_t groups{};
+    int64_t virtual_rows{};
+    bool preferred{};
+  };
+
   const vbsr_device_view& view() const { return view_; }
   const vbsr_row_schedule& schedule() const { return schedule_; }
+  const Split& split() const { return split_; }
 
 private:
   vbsr_device_view view_{};
   vbsr_row_schedule schedule_{};
+  Split split_{};
   std::vector<void*> allocations_;
   void release() noexcept;
 };
@@ -154,9 +192,20 @@ void launch_scalar(const vbsr_device_view& a, const float* b, float* c, int rhs,
 // empty schedule).  Requires row_owned_supported(a, b, c, rhs): float-aligned
 // B and C, and K small enough for 32-bit B offsets within a 16-column tile
 // (K <= 153,391,684 at rhs 8, 71,582,785 otherwise).
+bool row_owned_k_supported(const vbsr_device_view& a, int rhs);
 bool row_owned_supported(const vbsr_device_view& a, const float* b, const float* c, int rhs);
 void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& schedule, const float* b, float* c,
                       int rhs, hipStream_t stream);
+
+// The split-row path: the row-owned kernel over the matrix's split schedule
+// into `workspace` (split.virtual_rows * rhs floats), then the fixed-order
+// sum of each row's partial slabs into C.  Two launches; the workspace is
+// the caller's (a plan's own, or any buffer of at least that size that does
+// not overlap B or C).  Requires row_owned_supported(a, b, c, rhs).
+int64_t split_workspace_floats(const DeviceMatrix::Split& split, int rhs);
+void launch_split_row(const vbsr_device_view& a, const vbsr_row_schedule& schedule, const DeviceMatrix::Split& split,
+                      const float* b, float* c, int rhs, float* workspace, int64_t workspace_floats,
+                      hipStream_t stream);
 
 // ---- scalar CSR baseline on rocSPARSE (csr_baseline.cpp) ------------------
 
@@ -255,13 +304,27 @@ private:
 
 // ---- plan (plan.cpp) -------------------------------------------------------
 
-struct Plan {
-  vbsr_device_view a{};
-  vbsr_row_schedule schedule{};
-  vbsr_plan_options options{};
+// Plan (reference plan.cpp:5-31).  A plan on the split-row path owns its
+// workspace, allocated here and freed with the plan; execute allocates
+// nothing.
+class Plan {
+public:
   Plan(const DeviceMatrix& matrix, const vbsr_plan_options& options);
+  ~Plan();
+  Plan(const Plan&) = delete;
+  Plan& operator=(const Plan&) = delete;
   void execute(const float* b, float* c, hipStream_t stream) const;
   int launch_count() const;
+  bool split_row() const { return split_row_; }
+
+private:
+  vbsr_device_view a_{};
+  vbsr_row_schedule schedule_{};
+  DeviceMatrix::Split split_{};
+  vbsr_plan_options options_{};
+  bool split_row_{};
+  float* workspace_{};
+  int64_t workspace_floats_{};
 };
 
 }  // namespace vbsr_amd

@@ -169,9 +169,10 @@ struct Launch {
   vbsr_device_view a;
   const StepRec* steps;
   const WaveItem* items;  // kWaves per workgroup
-  int32_t step_limit;  // index of the last StepRec
+  int32_t step_limit;     // index of the last StepRec
   const float* b;
   float* c;
+  int64_t ldc;  // C's leading dimension: scalar_rows, or a split-row workspace's virtual rows
 };
 
 // Fixed-order reduction of the four partial slabs of a shared row,
@@ -382,7 +383,7 @@ __device__ __forceinline__ void row_body(const Launch& L, const WaveItem& item, 
   // A shared row's partial slabs are summed into wave 0's acc; a packed
   // row's wave already holds its row's sums.
   if (shared && !reduce_partials<RHS, T>(acc, lds, wave, lane)) return;
-  const int64_t ldc = L.a.scalar_rows;
+  const int64_t ldc = L.ldc;
   if constexpr (kDirect) {
     // Lane x holds rows 4 x .. 4 x + 3 of output columns 4 g + v: one
     // 16-byte store each, for the lanes whose rows are below h (a multiple
@@ -441,16 +442,59 @@ void launch(const Launch& L, int64_t groups, hipStream_t stream) {
   row_owned_mfma_kernel<RHS><<<dim3(unsigned(groups)), dim3(kThreads), 0, stream>>>(L);
 }
 
+void launch_items(const Launch& L, int64_t groups, int rhs, hipStream_t stream) {
+  if (groups <= 0) return;
+  if (groups > int64_t(0x7fffffff)) throw std::invalid_argument("schedule too large for one launch");
+  switch (rhs) {
+  case 8: launch<8>(L, groups, stream); break;
+  case 16: launch<16>(L, groups, stream); break;
+  case 32: launch<32>(L, groups, stream); break;
+  default: launch<64>(L, groups, stream); break;
+  }
+  check_hip(hipGetLastError(), "row_owned_mfma launch");
+}
+
+// Second pass of the split-row path: workgroup (i, j) sums the j-th run of
+// kReduceThreads elements of block row i's slab over the row's partial slabs
+// in part order, ((p0 + p1) + p2) + ..., and writes them to C.  Consecutive
+// lanes take consecutive rows of one RHS column, so each part's reads and the
+// C stores are contiguous; the loads of four parts are issued before their
+// adds, so a lane waits for memory once per four parts.
+constexpr int kReduceThreads = 256;
+
+__global__ __launch_bounds__(kReduceThreads) void split_reduce_kernel(const SplitRowRec* rows, const float* w,
+                                                                      int64_t ldw, float* c, int64_t ldc, int rhs) {
+  const SplitRowRec r = rows[blockIdx.x];
+  const int h = r.h;
+  const int e = int(blockIdx.y) * kReduceThreads + int(threadIdx.x);
+  if (e >= h * rhs) return;
+  const int n = e / h;
+  const int i = e - n * h;
+  const float* part = w + r.w_off + i + int64_t(n) * ldw;
+  float sum = part[0];
+  int q = 1;
+  for (; q + 3 < r.parts; q += 4) {
+    const float v0 = part[int64_t(q) * h], v1 = part[int64_t(q + 1) * h];
+    const float v2 = part[int64_t(q + 2) * h], v3 = part[int64_t(q + 3) * h];
+    sum = (((sum + v0) + v1) + v2) + v3;
+  }
+  for (; q < r.parts; ++q) sum += part[int64_t(q) * h];
+  c[r.c_off + i + int64_t(n) * ldc] = sum;
+}
+
 }  // namespace
 
-bool row_owned_supported(const vbsr_device_view& a, const float* b, const float* c, int rhs) {
-  // Float-aligned panels; 32-bit buffer offsets: a B tile's resource spans
-  // min(rhs, 16) - 1 columns of ld K plus one step, and must end at least
-  // 64 bytes below the out-of-range offset (K <= 153,391,684 at RHS 8,
-  // 71,582,785 otherwise).
+bool row_owned_k_supported(const vbsr_device_view& a, int rhs) {
+  // 32-bit buffer offsets: a B tile's resource spans min(rhs, 16) - 1
+  // columns of ld K plus one step, and must end at least 64 bytes below the
+  // out-of-range offset (K <= 153,391,684 at RHS 8, 71,582,785 otherwise).
   const uint64_t span = uint64_t(rhs < 16 ? rhs - 1 : 15) * uint64_t(a.scalar_cols) * 4u + 64u;
+  return span + 64u <= kOutOfRange;
+}
+
+bool row_owned_supported(const vbsr_device_view& a, const float* b, const float* c, int rhs) {
   return reinterpret_cast<uintptr_t>(b) % 4 == 0 && reinterpret_cast<uintptr_t>(c) % 4 == 0 &&
-         span + 64u <= kOutOfRange;
+         row_owned_k_supported(a, rhs);
 }
 
 void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& s, const float* b, float* c, int rhs,
@@ -460,17 +504,39 @@ void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& s, con
   if (!row_owned_supported(a, b, c, rhs))
     throw std::invalid_argument(
         "row-owned kernel needs (min(rhs, 16) - 1) * K * 4 + 128 <= 0xfffffff0 (its 32-bit B offsets)");
-  if (s.groups <= 0) return;
-  if (s.groups > int64_t(0x7fffffff)) throw std::invalid_argument("schedule too large for one launch");
   const void* rows = rhs >= 32 && s.rows_wide != nullptr ? s.rows_wide : s.rows;
-  const Launch L{a, static_cast<const StepRec*>(s.steps), static_cast<const WaveItem*>(rows), s.step_limit, b, c};
-  switch (rhs) {
-  case 8: launch<8>(L, s.groups, stream); break;
-  case 16: launch<16>(L, s.groups, stream); break;
-  case 32: launch<32>(L, s.groups, stream); break;
-  default: launch<64>(L, s.groups, stream); break;
+  const Launch L{a, static_cast<const StepRec*>(s.steps), static_cast<const WaveItem*>(rows), s.step_limit, b, c,
+                 a.scalar_rows};
+  launch_items(L, s.groups, rhs, stream);
+}
+
+int64_t split_workspace_floats(const DeviceMatrix::Split& split, int rhs) { return split.virtual_rows * rhs; }
+
+void launch_split_row(const vbsr_device_view& a, const vbsr_row_schedule& s, const DeviceMatrix::Split& split,
+                      const float* b, float* c, int rhs, float* workspace, int64_t workspace_floats,
+                      hipStream_t stream) {
+  if (!supported_rhs(rhs)) throw std::invalid_argument("unsupported rhs width");
+  check_panels(a, b, c, rhs);
+  if (!row_owned_supported(a, b, workspace, rhs))
+    throw std::invalid_argument(
+        "split-row path needs (min(rhs, 16) - 1) * K * 4 + 128 <= 0xfffffff0 (its 32-bit B offsets)");
+  const int64_t needed = split_workspace_floats(split, rhs);
+  if (needed > 0 && (workspace == nullptr || workspace_floats < needed))
+    throw std::invalid_argument("split-row workspace too small");
+  if (needed > 0) {
+    // The workspace must not overlap B or C.
+    check_panels(split.virtual_rows, a.scalar_cols, b, workspace, rhs);
+    check_panels(split.virtual_rows, a.scalar_rows, c, workspace, rhs);
   }
-  check_hip(hipGetLastError(), "row_owned_mfma launch");
+  if (a.block_rows <= 0) return;
+  const Launch L{a, static_cast<const StepRec*>(s.steps), split.items, s.step_limit, b, workspace,
+                 split.virtual_rows};
+  launch_items(L, split.groups, rhs, stream);
+  // A row's slab holds at most 64 * rhs elements.
+  const unsigned chunks = unsigned((64 * rhs + kReduceThreads - 1) / kReduceThreads);
+  split_reduce_kernel<<<dim3(unsigned(a.block_rows), chunks), dim3(kReduceThreads), 0, stream>>>(
+      split.rows, workspace, split.virtual_rows, c, a.scalar_rows, rhs);
+  check_hip(hipGetLastError(), "split_reduce launch");
 }
 
 }  // namespace vbsr_amd

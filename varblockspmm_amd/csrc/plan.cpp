@@ -3,34 +3,63 @@
 // The reference splits RHS-32 rows at h <= 16 into two CUDA launches and
 // picks a different CUDA kernel per width (row_owned.cu:333-358, 397-423).
 // On MI355X every width runs one launch of the row-owned MFMA kernel: a
-// workgroup owns a block row, its four waves share the row's k steps and
-// reduce their partial tiles in LDS, so the row height no longer decides the
-// kernel and the height split has no counterpart.  The matrix's row schedule
-// (schedule.cpp) orders and places the rows instead.
+// workgroup owns a block row (or four light ones, one per wave), its waves
+// share the row's k steps and reduce their partial tiles in LDS, so the row
+// height no longer decides the kernel and the height split has no
+// counterpart.  The matrix's row schedule (schedule.cpp) orders and places
+// the rows instead.
+//
+// Kernel::SplitRow, reserved in the reference (plan.cpp:13-17), is the
+// split-row path here: each row's k steps are cut into parts computed by the
+// same kernel into a plan-owned workspace, and a second launch sums each
+// row's parts in a fixed order.  Kernel::Auto takes it for matrices whose
+// row-owned launch would leave most CUs idle while their rows are long (few
+// block rows of high degree); Kernel::RowOwned never does.
 //
 // Matrices with more scalar columns than the MFMA kernel's 32-bit B offsets
 // reach (K > 153,391,684 at RHS 8, K > 71,582,785 otherwise) go to the
-// order-preserving kernel, which has no such limit.  Any float-aligned B and C panels stay on the MFMA kernel.
+// order-preserving kernel, which has no such limit.  Any float-aligned B and
+// C panels stay on the MFMA kernel.
+#include <hip/hip_runtime_api.h>
+
 #include "internal.hpp"
 
 namespace vbsr_amd {
 
 Plan::Plan(const DeviceMatrix& matrix, const vbsr_plan_options& o)
-    : a(matrix.view()), schedule(matrix.schedule()), options(o) {
+    : a_(matrix.view()), schedule_(matrix.schedule()), split_(matrix.split()), options_(o) {
   if (!supported_rhs(o.rhs_width)) throw std::invalid_argument("rhs_width must be 8,16,32,64");
-  if (o.kernel == VBSR_KERNEL_SPLIT_ROW)
-    throw std::invalid_argument("split-row is reserved and not provided; use RowOwned");
-  if (o.kernel != VBSR_KERNEL_AUTO && o.kernel != VBSR_KERNEL_ROW_OWNED)
+  if (o.kernel != VBSR_KERNEL_AUTO && o.kernel != VBSR_KERNEL_ROW_OWNED && o.kernel != VBSR_KERNEL_SPLIT_ROW)
     throw std::invalid_argument("unknown kernel selection");
+  split_row_ = o.kernel == VBSR_KERNEL_SPLIT_ROW || (o.kernel == VBSR_KERNEL_AUTO && split_.preferred);
+  if (split_row_) {
+    workspace_floats_ = split_workspace_floats(split_, o.rhs_width);
+    if (workspace_floats_ > 0)
+      check_hip(hipMalloc(reinterpret_cast<void**>(&workspace_), size_t(workspace_floats_) * sizeof(float)),
+                "hipMalloc (split-row workspace)");
+  }
+}
+
+Plan::~Plan() {
+  if (workspace_ != nullptr) (void)hipFree(workspace_);
 }
 
 void Plan::execute(const float* b, float* c, hipStream_t stream) const {
-  if (row_owned_supported(a, b, c, options.rhs_width))
-    launch_row_owned(a, schedule, b, c, options.rhs_width, stream);
+  if (!row_owned_supported(a_, b, c, options_.rhs_width))
+    launch_scalar(a_, b, c, options_.rhs_width, stream);
+  else if (split_row_)
+    launch_split_row(a_, schedule_, split_, b, c, options_.rhs_width, workspace_, workspace_floats_, stream);
   else
-    launch_scalar(a, b, c, options.rhs_width, stream);
+    launch_row_owned(a_, schedule_, b, c, options_.rhs_width, stream);
 }
 
-int Plan::launch_count() const { return schedule.groups > 0 ? 1 : 0; }
+int Plan::launch_count() const {
+  if (a_.block_rows <= 0) return 0;
+  // The order-preserving kernel (K beyond the MFMA kernel's offsets) is one
+  // launch.
+  if (!row_owned_k_supported(a_, options_.rhs_width)) return 1;
+  if (split_row_) return 2;
+  return schedule_.groups > 0 ? 1 : 0;
+}
 
 }  // namespace vbsr_amd
