@@ -207,6 +207,20 @@ int vbsr_split_row_workspace_bytes(const vbsr_matrix* matrix, int32_t rhs, int64
 int vbsr_launch_split_row(const vbsr_matrix* matrix, const float* B, float* C, int32_t rhs, void* workspace,
                           int64_t workspace_bytes, hipStream_t stream);
 
+/* vbsr_launch_split_row without a workspace argument; no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): the
+ * partial slabs go to the library's static device scratch, 16 MiB per device
+ * (set aside when the library is loaded on the device, held until the
+ * process ends), so the call allocates nothing.  A matrix whose workspace
+ * (vbsr_split_row_workspace_bytes) exceeds 16 MiB is rejected
+ * (VBSR_INVALID_ARGUMENT) before any launch.  Every call on a device shares
+ * that device's scratch: calls that overlap in time on one device race, so
+ * serialise them (one stream, or events).  Results are bit-identical to
+ * vbsr_launch_split_row's. */
+int vbsr_launch_split_row_static(const vbsr_matrix* matrix, const float* B, float* C, int32_t rhs,
+                                 hipStream_t stream);
+
 /* launch_row_owned_scalar (vbsr.hpp:161; row_owned.cu:376-395): one output
  * per lane, accumulated with fmaf over blocks in row_ptr order and k
  * ascending from 0 -- the reference kernels' exact order, so its results are

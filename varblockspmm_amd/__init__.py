@@ -88,6 +88,7 @@ SIGNATURES = {
     "vbsr_launch_row_owned_scalar": (ctypes.c_int, [ctypes.POINTER(DeviceView), _P, _P, ctypes.c_int32, _P]),
     "vbsr_split_row_workspace_bytes": (ctypes.c_int, [_P, ctypes.c_int32, ctypes.POINTER(ctypes.c_int64)]),
     "vbsr_launch_split_row": (ctypes.c_int, [_P, _P, _P, ctypes.c_int32, _P, ctypes.c_int64, _P]),
+    "vbsr_launch_split_row_static": (ctypes.c_int, [_P, _P, _P, ctypes.c_int32, _P]),
     "vbsr_csr_plan_create": (ctypes.c_int, [ctypes.POINTER(HostView), ctypes.c_int32, ctypes.POINTER(_P)]),
     "vbsr_csr_plan_destroy": (None, [_P]),
     "vbsr_csr_plan_execute": (ctypes.c_int, [_P, _P, _P, _P]),
@@ -353,6 +354,15 @@ def launch_split_row(matrix, B, C, rhs, workspace, workspace_bytes=None, stream=
         workspace_bytes = workspace.numel() * workspace.element_size() if hasattr(workspace, "numel") else 0
     _check(library().vbsr_launch_split_row(matrix._handle, _address(B), _address(C), int(rhs), _address(workspace),
                                            int(workspace_bytes), _stream(stream)))
+
+
+def launch_split_row_static(matrix, B, C, rhs, stream=None):
+    """The split-row path with the library's static device scratch as its workspace (16 MiB per device):
+    allocates nothing; calls that overlap on one device race."""
+    _check_panel(B, matrix.scalar_cols * int(rhs), "B")
+    _check_panel(C, matrix.scalar_rows * int(rhs), "C")
+    _check(library().vbsr_launch_split_row_static(matrix._handle, _address(B), _address(C), int(rhs),
+                                                  _stream(stream)))
 
 
 class ScalarCsrPlan:

@@ -191,6 +191,15 @@ int vbsr_launch_split_row(const vbsr_matrix* matrix, const float* B, float* C, i
   });
 }
 
+int vbsr_launch_split_row_static(const vbsr_matrix* matrix, const float* B, float* C, int32_t rhs,
+                                 hipStream_t stream) {
+  return guarded([&] {
+    require(matrix, "matrix");
+    vbsr_amd::launch_split_row_static(matrix->device.view(), matrix->device.schedule(), matrix->device.split(), B, C,
+                                      rhs, stream);
+  });
+}
+
 int vbsr_launch_row_owned_scalar(const vbsr_device_view* matrix, const float* B, float* C, int32_t rhs,
                                  hipStream_t stream) {
   return guarded([&] {

@@ -206,6 +206,13 @@ int64_t split_workspace_floats(const DeviceMatrix::Split& split, int rhs);
 void launch_split_row(const vbsr_device_view& a, const vbsr_row_schedule& schedule, const DeviceMatrix::Split& split,
                       const float* b, float* c, int rhs, float* workspace, int64_t workspace_floats,
                       hipStream_t stream);
+// The same with the library's static device scratch (split_scratch_floats()
+// floats per device) as the workspace: allocates nothing, and rejects a
+// matrix whose workspace would not fit.  Calls on one device share the
+// scratch, so calls that overlap in time on one device race.
+int64_t split_scratch_floats();
+void launch_split_row_static(const vbsr_device_view& a, const vbsr_row_schedule& schedule,
+                             const DeviceMatrix::Split& split, const float* b, float* c, int rhs, hipStream_t stream);
 
 // ---- scalar CSR baseline on rocSPARSE (csr_baseline.cpp) ------------------
 

@@ -64,6 +64,9 @@
 // MFMAs.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+#include <string>
+
 #include "../internal.hpp"
 
 namespace vbsr_amd {
@@ -482,6 +485,32 @@ __global__ __launch_bounds__(kReduceThreads) void split_reduce_kernel(const Spli
   c[r.c_off + i + int64_t(n) * ldc] = sum;
 }
 
+// The allocation-free split-row launcher's workspace: one static array per
+// device, 16 MiB, set aside when the library's code object is loaded on the
+// device and held until the process ends.  Host code never passes `scratch`
+// itself to a kernel (on the host it names a stand-in, not device memory):
+// it passes the device address that hipGetSymbolAddress returns for the
+// current device, looked up once per device.
+constexpr int64_t kScratchFloats = int64_t(4) << 20;
+__device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch[kMaxDevices] = {};
+
+float* scratch_for_current_device() {
+  int device = 0;
+  check_hip(hipGetDevice(&device), "hipGetDevice");
+  if (device < 0 || device >= kMaxDevices) throw std::runtime_error("device ordinal beyond the scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch[device] == nullptr) {
+    void* address = nullptr;
+    check_hip(hipGetSymbolAddress(&address, HIP_SYMBOL(scratch)), "hipGetSymbolAddress (split-row scratch)");
+    g_scratch[device] = static_cast<float*>(address);
+  }
+  return g_scratch[device];
+}
+
 }  // namespace
 
 bool row_owned_k_supported(const vbsr_device_view& a, int rhs) {
@@ -537,6 +566,19 @@ void launch_split_row(const vbsr_device_view& a, const vbsr_row_schedule& s, con
   split_reduce_kernel<<<dim3(unsigned(a.block_rows), chunks), dim3(kReduceThreads), 0, stream>>>(
       split.rows, workspace, split.virtual_rows, c, a.scalar_rows, rhs);
   check_hip(hipGetLastError(), "split_reduce launch");
+}
+
+int64_t split_scratch_floats() { return kScratchFloats; }
+
+void launch_split_row_static(const vbsr_device_view& a, const vbsr_row_schedule& s, const DeviceMatrix::Split& split,
+                             const float* b, float* c, int rhs, hipStream_t stream) {
+  if (!supported_rhs(rhs)) throw std::invalid_argument("unsupported rhs width");
+  const int64_t needed = split_workspace_floats(split, rhs);
+  if (needed > kScratchFloats)
+    throw std::invalid_argument("split-row workspace of " + std::to_string(needed * 4) +
+                                " bytes exceeds the static scratch (" + std::to_string(kScratchFloats * 4) +
+                                " bytes); use vbsr_launch_split_row with a workspace");
+  launch_split_row(a, s, split, b, c, rhs, scratch_for_current_device(), kScratchFloats, stream);
 }
 
 }  // namespace vbsr_amd
