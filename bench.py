@@ -53,8 +53,9 @@ def parse():
     p.add_argument("--locality", default="random")
     p.add_argument("--rhs", type=int, default=32)
     p.add_argument("--seed", type=int, default=1)
-    p.add_argument("--kernel", choices=["plan", "scalar"], default="plan",
-                   help="plan = the library's Plan::execute; scalar = the order-preserving kernel")
+    p.add_argument("--kernel", choices=["plan", "scalar", "valu"], default="plan",
+                   help="plan = the library's Plan::execute; scalar = the order-preserving kernel; valu = the "
+                        "row-owned kernel with plain FP32 multiply-adds instead of MFMA (the measured alternative)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-parity", action="store_true")
     p.add_argument("--calibrate-copy-mib", type=int, default=0,
@@ -214,9 +215,13 @@ def main():
     sink = torch.empty((), dtype=torch.float32, device=device)
     torch.cuda.synchronize()
 
+    schedule = matrix.row_schedule()
+
     def step():
         if args.kernel == "plan":
             plan.execute(b_dev, c_dev, stream)
+        elif args.kernel == "valu":
+            vb.launch_row_owned_valu(view, schedule, b_dev, c_dev, args.rhs, stream)
         else:
             vb.launch_row_owned_scalar(view, b_dev, c_dev, args.rhs, stream)
 

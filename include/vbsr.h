@@ -192,6 +192,14 @@ int vbsr_plan_launch_count(const vbsr_plan* plan);
 int vbsr_launch_row_owned(const vbsr_device_view* matrix, const vbsr_row_schedule* schedule,
                           const float* B, float* C, int32_t rhs, hipStream_t stream);
 
+/* vbsr_launch_row_owned with plain FP32 multiply-adds (one fmaf per output
+ * and k, k ascending within each step) in place of the MFMA tiles: the same
+ * schedule, loads and LDS staging, within the same tolerance.  No
+ * counterpart in the reference; kept as the measured alternative to the
+ * MFMA kernel, which is faster at every RHS width (bench.py --kernel valu). */
+int vbsr_launch_row_owned_valu(const vbsr_device_view* matrix, const vbsr_row_schedule* schedule,
+                               const float* B, float* C, int32_t rhs, hipStream_t stream);
+
 /* The split-row path (the reference's reserved Kernel::SplitRow,
  * vbsr.hpp:91, plan.cpp:13-17).  Each block row's k steps are cut into parts
  * (the matrix's split schedule, built at vbsr_matrix_create); the row-owned

@@ -400,6 +400,27 @@ def test_order_preserving_kernel_gives_the_closed_form_bits(probe):
     c.close()
 
 
+# ---- the VALU variant of the row-owned kernel (the measured alternative to MFMA) ----------------
+
+
+@pytest.mark.parametrize("case", reference_cases()[::5] + [("high", 8, rhs, "random", 1) for rhs in (8, 16, 32, 64)],
+                         ids=lambda c: "{}-d{}-n{}-{}-s{}".format(*c))
+def test_valu_variant_matches_the_oracle(case):
+    """launch_row_owned_valu: the same schedule with plain FP32 multiply-adds; within tolerance of the
+    oracle and bit-identical across runs (every thirteenth reference case, or so, and configuration 3's
+    matrix at 1,024 block rows at every width)."""
+    distribution, degree, rhs, locality, seed = case
+    rows, cols = (9, 17) if seed != 1 else (1024, 1024)
+    note(f"valu case {case}")
+    c = Case(vb.generate(rows, cols, degree, distribution, locality, seed), rhs, seed)
+    view, schedule = c.matrix.device_view(), c.matrix.row_schedule()
+    launch = lambda: vb.launch_row_owned_valu(view, schedule, c.b_dev, c.c_dev, rhs, c.stream)
+    first = c.run(launch)
+    c.check_tolerance(first, "valu")
+    np.testing.assert_array_equal(c.run(launch), first)
+    c.close()
+
+
 # ---- the split-row path (the reference's reserved Kernel::SplitRow) -----------------------------
 
 

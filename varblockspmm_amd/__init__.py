@@ -86,6 +86,8 @@ SIGNATURES = {
     "vbsr_launch_row_owned": (ctypes.c_int, [ctypes.POINTER(DeviceView), ctypes.POINTER(RowSchedule), _P, _P,
                                              ctypes.c_int32, _P]),
     "vbsr_launch_row_owned_scalar": (ctypes.c_int, [ctypes.POINTER(DeviceView), _P, _P, ctypes.c_int32, _P]),
+    "vbsr_launch_row_owned_valu": (ctypes.c_int, [ctypes.POINTER(DeviceView), ctypes.POINTER(RowSchedule), _P, _P,
+                                                  ctypes.c_int32, _P]),
     "vbsr_split_row_workspace_bytes": (ctypes.c_int, [_P, ctypes.c_int32, ctypes.POINTER(ctypes.c_int64)]),
     "vbsr_launch_split_row": (ctypes.c_int, [_P, _P, _P, ctypes.c_int32, _P, ctypes.c_int64, _P]),
     "vbsr_launch_split_row_static": (ctypes.c_int, [_P, _P, _P, ctypes.c_int32, _P]),
@@ -328,6 +330,14 @@ def launch_row_owned(device_view, schedule, B, C, rhs, stream=None):
     _check_panel(C, device_view.scalar_rows * int(rhs), "C")
     _check(library().vbsr_launch_row_owned(ctypes.byref(device_view), ctypes.byref(schedule), _address(B),
                                            _address(C), int(rhs), _stream(stream)))
+
+
+def launch_row_owned_valu(device_view, schedule, B, C, rhs, stream=None):
+    """The row-owned kernel with plain FP32 multiply-adds instead of MFMA tiles (the measured alternative)."""
+    _check_panel(B, device_view.scalar_cols * int(rhs), "B")
+    _check_panel(C, device_view.scalar_rows * int(rhs), "C")
+    _check(library().vbsr_launch_row_owned_valu(ctypes.byref(device_view), ctypes.byref(schedule), _address(B),
+                                                _address(C), int(rhs), _stream(stream)))
 
 
 def launch_row_owned_scalar(device_view, B, C, rhs, stream=None):

@@ -200,6 +200,15 @@ int vbsr_launch_split_row_static(const vbsr_matrix* matrix, const float* B, floa
   });
 }
 
+int vbsr_launch_row_owned_valu(const vbsr_device_view* matrix, const vbsr_row_schedule* schedule, const float* B,
+                               float* C, int32_t rhs, hipStream_t stream) {
+  return guarded([&] {
+    require(matrix, "matrix");
+    require(schedule, "schedule");
+    vbsr_amd::launch_row_owned_valu(*matrix, *schedule, B, C, rhs, stream);
+  });
+}
+
 int vbsr_launch_row_owned_scalar(const vbsr_device_view* matrix, const float* B, float* C, int32_t rhs,
                                  hipStream_t stream) {
   return guarded([&] {

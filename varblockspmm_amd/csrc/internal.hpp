@@ -192,6 +192,11 @@ void launch_scalar(const vbsr_device_view& a, const float* b, float* c, int rhs,
 // empty schedule).  Requires row_owned_supported(a, b, c, rhs): float-aligned
 // B and C, and K small enough for 32-bit B offsets within a 16-column tile
 // (K <= 153,391,684 at rhs 8, 71,582,785 otherwise).
+// The same kernel with the MFMA tiles replaced by one fmaf per output and k
+// (same schedule, loads and LDS staging): the measured alternative to MFMA,
+// slower at every width.
+void launch_row_owned_valu(const vbsr_device_view& a, const vbsr_row_schedule& schedule, const float* b, float* c,
+                           int rhs, hipStream_t stream);
 bool row_owned_k_supported(const vbsr_device_view& a, int rhs);
 bool row_owned_supported(const vbsr_device_view& a, const float* b, const float* c, int rhs);
 void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& schedule, const float* b, float* c,

@@ -110,15 +110,22 @@ constexpr int rhs_tiles() {
   return RHS < 16 ? 1 : RHS / 16;
 }
 
+// The VALU variant's k-major B slot: floats per k of one RHS tile (16
+// columns and 4 of padding, so that the transposing writes of lanes 4 n + q
+// land in 64 distinct banks).
+constexpr int kValuBLd = 20;
+
 // LDS of one workgroup: one area per wave holding its B slot and its A slot.
 // The reduction's partial slabs reuse the areas of the waves that leave
 // them (their main loops are over by then), which are sized for them.
-template <int RHS>
+// kValu: the VALU variant's B slot is k-major with 20 floats per k (1280
+// bytes per RHS tile), and its A slot always holds four tiles.
+template <int RHS, bool kValu>
 struct Lds {
-  static constexpr int kBBytes = rhs_tiles<RHS>() * kWave * 16;
-  // Row tiles that go through the A slot: at RHS 8, four-tile rows read A
-  // straight into registers.
-  static constexpr int kSlotTiles = RHS == 8 ? kMaxTiles - 1 : kMaxTiles;
+  static constexpr int kBBytes = rhs_tiles<RHS>() * (kValu ? 16 * kValuBLd * 4 : kWave * 16);
+  // Row tiles that go through the A slot: at RHS 8 the MFMA path reads
+  // four-tile rows straight into registers.
+  static constexpr int kSlotTiles = RHS == 8 && !kValu ? kMaxTiles - 1 : kMaxTiles;
   static constexpr int kABytes = 16 * (16 * kSlotTiles + 4) * 4;
   static constexpr int kSlotBytes = kBBytes + kABytes;
   static constexpr int kPartialBytes = kMaxTiles * rhs_tiles<RHS>() * kWave * 16;
@@ -182,9 +189,9 @@ struct Launch {
 // (w0 + w2) + (w1 + w3), after every wave's main loop.  Afterwards wave 0's
 // acc holds the row's sums; returns true for wave 0 only.  The whole
 // workgroup shares the row, so every wave reaches the barriers.
-template <int RHS, int T>
+template <int RHS, int T, bool kValu>
 __device__ __forceinline__ bool reduce_partials(f32x4 (&acc)[T][rhs_tiles<RHS>()], char* lds, int wave, int lane) {
-  using Layout = Lds<RHS>;
+  using Layout = Lds<RHS, kValu>;
   constexpr int kRhsTiles = rhs_tiles<RHS>();
   f32x4* part1 = reinterpret_cast<f32x4*>(lds + Layout::area(1));
   f32x4* part2 = reinterpret_cast<f32x4*>(lds + Layout::area(2));
@@ -241,9 +248,54 @@ __device__ __forceinline__ bool reduce_partials(f32x4 (&acc)[T][rhs_tiles<RHS>()
   return true;
 }
 
+// One k step of the VALU variant: B goes into the k-major slot (lane 4 n + q
+// holds B[k0 + 4 q + e, n0 + n], e < 4), then lane (g, x) accumulates rows
+// 16 t + x of RHS columns [g * RHS / 4, (g + 1) * RHS / 4) with one fmaf per
+// output and k, k ascending: 16 T RHS / 4 multiply-adds per lane per step,
+// on the same A slot as the MFMA path.  The 16 lanes of a group read the
+// same B address (a broadcast) and 16 consecutive A rows.
 template <int RHS, int T>
+__device__ __forceinline__ void valu_step(const f32x4 (&b)[rhs_tiles<RHS>()], float* bk, const float* a_slot,
+                                          f32x4 (&acc)[T][rhs_tiles<RHS>()], int group, int x, int b_n, int b_q,
+                                          int last_rows) {
+  constexpr int kRhsTiles = rhs_tiles<RHS>();
+  constexpr int ld = 16 * T + 4;
+  constexpr int kTile = 16 * kValuBLd;
+#pragma unroll
+  for (int nt = 0; nt < kRhsTiles; ++nt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) bk[nt * kTile + (4 * b_q + e) * kValuBLd + b_n] = b[nt][e];
+  constexpr int kCols = RHS / 4;
+  const int tile = (group * kCols) / 16;
+  const int n0 = (group * kCols) % 16;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    float bv[kCols];
+    if constexpr (kCols >= 4) {
+#pragma unroll
+      for (int j = 0; j < kCols; j += 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(bk + (tile + j / 16) * kTile + k * kValuBLd + (n0 + j) % 16);
+        bv[j] = v[0];
+        bv[j + 1] = v[1];
+        bv[j + 2] = v[2];
+        bv[j + 3] = v[3];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kCols; ++j) bv[j] = bk[tile * kTile + k * kValuBLd + n0 + j];
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const float av = t < T - 1 ? a_slot[k * ld + 16 * t + x] : a_slot[k * ld + 16 * (T - 1) + (x & (last_rows - 1))];
+#pragma unroll
+      for (int j = 0; j < kCols; ++j) acc[t][j / 4][j % 4] = __builtin_fmaf(av, bv[j], acc[t][j / 4][j % 4]);
+    }
+  }
+}
+
+template <int RHS, int T, bool kValu>
 __device__ __forceinline__ void row_body(const Launch& L, const WaveItem& item, char* lds, int wave, int lane) {
-  using Layout = Lds<RHS>;
+  using Layout = Lds<RHS, kValu>;
   constexpr int kRhsTiles = rhs_tiles<RHS>();
   constexpr int kRhsLanes = RHS < 16 ? RHS : 16;
   constexpr int ld = 16 * T + 4;  // A slot: float (r, k) of the step at k * ld + r
@@ -263,7 +315,7 @@ __device__ __forceinline__ void row_body(const Launch& L, const WaveItem& item, 
   char* area = lds + Layout::area(wave);
   f32x4* b_slot = reinterpret_cast<f32x4*>(area);
   float* a_slot = reinterpret_cast<float*>(area + Layout::kBBytes);
-  constexpr bool kDirect = RHS == 8 && T == kMaxTiles;  // A straight into MFMA layout
+  constexpr bool kDirect = !kValu && RHS == 8 && T == kMaxTiles;  // A straight into MFMA layout
   static_assert(kDirect || T <= Layout::kSlotTiles, "the A slot holds the rows that use it");
   // Direct path: load i of lane 16 g + x reads rows 4 x .. 4 x + 3 of block
   // column 4 g + i.
@@ -347,6 +399,10 @@ __device__ __forceinline__ void row_body(const Launch& L, const WaveItem& item, 
 #pragma unroll
         for (int q = 0; q < T; ++q) *reinterpret_cast<f32x4*>(a_slot + a_write[q]) = st.a[q];
       }
+      if constexpr (kValu) {
+        valu_step<RHS, T>(st.b, reinterpret_cast<float*>(b_slot), a_slot, acc, group, x, b_n, b_q, last_rows);
+        return;
+      }
 #pragma unroll
       for (int nt = 0; nt < kRhsTiles; ++nt) b_slot[nt * kWave + slot_write] = st.b[nt];
       f32x4 bv[kRhsTiles];
@@ -385,7 +441,7 @@ __device__ __forceinline__ void row_body(const Launch& L, const WaveItem& item, 
 
   // A shared row's partial slabs are summed into wave 0's acc; a packed
   // row's wave already holds its row's sums.
-  if (shared && !reduce_partials<RHS, T>(acc, lds, wave, lane)) return;
+  if (shared && !reduce_partials<RHS, T, kValu>(acc, lds, wave, lane)) return;
   const int64_t ldc = L.ldc;
   if constexpr (kDirect) {
     // Lane x holds rows 4 x .. 4 x + 3 of output columns 4 g + v: one
@@ -407,6 +463,16 @@ __device__ __forceinline__ void row_body(const Launch& L, const WaveItem& item, 
     return;
   }
   float* c_row = L.c + item.c_off + x;
+  if constexpr (kValu) {
+    // Lane (g, x) holds rows 16 t + x of RHS columns g * RHS / 4 + j.
+    constexpr int kCols = RHS / 4;
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      if (t < T - 1 || x < last_rows)
+#pragma unroll
+        for (int j = 0; j < kCols; ++j) c_row[16 * t + int64_t(group * kCols + j) * ldc] = acc[t][j / 4][j % 4];
+    return;
+  }
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     if (t < T - 1 || x < last_rows) {
@@ -423,9 +489,9 @@ __device__ __forceinline__ void row_body(const Launch& L, const WaveItem& item, 
   }
 }
 
-template <int RHS>
+template <int RHS, bool kValu>
 __global__ __launch_bounds__(kThreads) void row_owned_mfma_kernel(Launch L) {
-  __shared__ __attribute__((aligned(16))) char lds[Lds<RHS>::kTotal];
+  __shared__ __attribute__((aligned(16))) char lds[Lds<RHS, kValu>::kTotal];
   const int wave = uniform(int(threadIdx.x) / kWave);
   const int lane = int(threadIdx.x) % kWave;
   const WaveItem item = L.items[int64_t(blockIdx.x) * kWaves + wave];
@@ -433,26 +499,27 @@ __global__ __launch_bounds__(kThreads) void row_owned_mfma_kernel(Launch L) {
   // so no wave that leaves here is awaited at a barrier.
   if (uniform(item.step_count) < 0) return;
   switch ((uniform(item.h) + 15) >> 4) {
-  case 1: row_body<RHS, 1>(L, item, lds, wave, lane); break;
-  case 2: row_body<RHS, 2>(L, item, lds, wave, lane); break;
-  case 3: row_body<RHS, 3>(L, item, lds, wave, lane); break;
-  default: row_body<RHS, 4>(L, item, lds, wave, lane); break;
+  case 1: row_body<RHS, 1, kValu>(L, item, lds, wave, lane); break;
+  case 2: row_body<RHS, 2, kValu>(L, item, lds, wave, lane); break;
+  case 3: row_body<RHS, 3, kValu>(L, item, lds, wave, lane); break;
+  default: row_body<RHS, 4, kValu>(L, item, lds, wave, lane); break;
   }
 }
 
-template <int RHS>
+template <int RHS, bool kValu>
 void launch(const Launch& L, int64_t groups, hipStream_t stream) {
-  row_owned_mfma_kernel<RHS><<<dim3(unsigned(groups)), dim3(kThreads), 0, stream>>>(L);
+  row_owned_mfma_kernel<RHS, kValu><<<dim3(unsigned(groups)), dim3(kThreads), 0, stream>>>(L);
 }
 
+template <bool kValu>
 void launch_items(const Launch& L, int64_t groups, int rhs, hipStream_t stream) {
   if (groups <= 0) return;
   if (groups > int64_t(0x7fffffff)) throw std::invalid_argument("schedule too large for one launch");
   switch (rhs) {
-  case 8: launch<8>(L, groups, stream); break;
-  case 16: launch<16>(L, groups, stream); break;
-  case 32: launch<32>(L, groups, stream); break;
-  default: launch<64>(L, groups, stream); break;
+  case 8: launch<8, kValu>(L, groups, stream); break;
+  case 16: launch<16, kValu>(L, groups, stream); break;
+  case 32: launch<32, kValu>(L, groups, stream); break;
+  default: launch<64, kValu>(L, groups, stream); break;
   }
   check_hip(hipGetLastError(), "row_owned_mfma launch");
 }
@@ -526,8 +593,11 @@ bool row_owned_supported(const vbsr_device_view& a, const float* b, const float*
          row_owned_k_supported(a, rhs);
 }
 
-void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& s, const float* b, float* c, int rhs,
-                      hipStream_t stream) {
+namespace {
+
+template <bool kValu>
+void launch_row_owned_math(const vbsr_device_view& a, const vbsr_row_schedule& s, const float* b, float* c, int rhs,
+                           hipStream_t stream) {
   if (!supported_rhs(rhs)) throw std::invalid_argument("unsupported rhs width");
   check_panels(a, b, c, rhs);
   if (!row_owned_supported(a, b, c, rhs))
@@ -536,7 +606,19 @@ void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& s, con
   const void* rows = rhs >= 32 && s.rows_wide != nullptr ? s.rows_wide : s.rows;
   const Launch L{a, static_cast<const StepRec*>(s.steps), static_cast<const WaveItem*>(rows), s.step_limit, b, c,
                  a.scalar_rows};
-  launch_items(L, s.groups, rhs, stream);
+  launch_items<kValu>(L, s.groups, rhs, stream);
+}
+
+}  // namespace
+
+void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& s, const float* b, float* c, int rhs,
+                      hipStream_t stream) {
+  launch_row_owned_math<false>(a, s, b, c, rhs, stream);
+}
+
+void launch_row_owned_valu(const vbsr_device_view& a, const vbsr_row_schedule& s, const float* b, float* c, int rhs,
+                           hipStream_t stream) {
+  launch_row_owned_math<true>(a, s, b, c, rhs, stream);
 }
 
 int64_t split_workspace_floats(const DeviceMatrix::Split& split, int rhs) { return split.virtual_rows * rhs; }
@@ -560,7 +642,7 @@ void launch_split_row(const vbsr_device_view& a, const vbsr_row_schedule& s, con
   if (a.block_rows <= 0) return;
   const Launch L{a, static_cast<const StepRec*>(s.steps), split.items, s.step_limit, b, workspace,
                  split.virtual_rows};
-  launch_items(L, split.groups, rhs, stream);
+  launch_items<false>(L, split.groups, rhs, stream);
   // A row's slab holds at most 64 * rhs elements.
   const unsigned chunks = unsigned((64 * rhs + kReduceThreads - 1) / kReduceThreads);
   split_reduce_kernel<<<dim3(unsigned(a.block_rows), chunks), dim3(kReduceThreads), 0, stream>>>(
