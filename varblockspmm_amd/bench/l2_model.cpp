@@ -58,6 +58,7 @@ struct Options {
   double l2_mib = 4.0, c0 = 6.0, c1 = 1.0;
   int ways = 16;
   int c_allocates = 1;
+  std::string b_layout = "columns";
 };
 
 int parse_distribution(const std::string& s) {
@@ -139,6 +140,7 @@ int main(int argc, char** argv) {
     else if (k == "--c0") o.c0 = std::atof(v);
     else if (k == "--c1") o.c1 = std::atof(v);
     else if (k == "--c-allocates") o.c_allocates = std::atoi(v);
+    else if (k == "--b-layout") o.b_layout = v;
     else {
       std::fprintf(stderr, "unknown option %s\n", k.c_str());
       return 2;
@@ -191,10 +193,16 @@ int main(int argc, char** argv) {
           const int run = j / kStepRun;
           const int position = (run / p) * kStepRun + j % kStepRun;  // the step's place in its wave
           const double t = start + o.c0 * 0.5 + o.c1 * position + 1e-6 * (j % 7);
-          for (int n = 0; n < o.rhs; ++n) {
-            const int64_t first = (b_base + (n * K + k0) * 4) / kLine;
-            const int64_t last = (b_base + (n * K + k0 + len) * 4 - 1) / kLine;
+          if (o.b_layout == "rows") {
+            const int64_t first = (b_base + k0 * o.rhs * 4) / kLine;
+            const int64_t last = (b_base + (k0 + len) * o.rhs * 4 - 1) / kLine;
             for (int64_t line = first; line <= last; ++line) events.push_back({t, line, true});
+          } else {
+            for (int n = 0; n < o.rhs; ++n) {
+              const int64_t first = (b_base + (n * K + k0) * 4) / kLine;
+              const int64_t last = (b_base + (n * K + k0 + len) * 4 - 1) / kLine;
+              for (int64_t line = first; line <= last; ++line) events.push_back({t, line, true});
+            }
           }
         }
       }

@@ -65,6 +65,8 @@ def main(argv=None):
     p.add_argument("--input", choices=["constant", "random"], default="constant")
     p.add_argument("--no-cold", action="store_true", help="skip the cold-cache repetitions")
     p.add_argument("--limit", type=int, default=0, help="run only the first N cases")
+    p.add_argument("--kernel", choices=["auto", "row_owned", "split_row"], default="auto",
+                   help="the plan's kernel selection (auto: the product's default)")
     p.add_argument("--exe", default=EXECUTABLE)
     args = p.parse_args(argv)
     if not os.path.exists(args.exe):
@@ -78,7 +80,7 @@ def main(argv=None):
             command = [args.exe, "--rows", str(args.rows), "--degree", str(case["degree"]), "--rhs", str(case["rhs"]),
                        "--distribution", case["distribution"], "--locality", case["locality"],
                        "--reps", str(args.reps), "--warmup", str(args.warmup), "--seed", str(case["seed"]),
-                       "--input", args.input]
+                       "--input", args.input, "--kernel", args.kernel]
             if args.no_cold:
                 command.append("--no-cold")
             if index > 0:
