@@ -157,9 +157,7 @@ typedef struct vbsr_row_schedule {
   const void* rows;      /* device: four 48-byte wave items per workgroup, launch order for rhs 8 and 16 */
   int64_t groups;        /* workgroups of one launch */
   int32_t step_limit;    /* index of the last step record */
-  const void* rows_wide; /* device: the same row items, launch order for rhs 32 (and the VALU variant at 64) */
-  const void* rows_tile; /* device: one 48-byte wave item per workgroup, launch order of the rhs 64 kernel */
-  int64_t groups_tile;   /* workgroups of the rhs 64 launch */
+  const void* rows_wide; /* device: the same row items, launch order for rhs 32 and 64 */
 } vbsr_row_schedule;
 int vbsr_matrix_row_schedule(const vbsr_matrix* matrix, vbsr_row_schedule* out);
 

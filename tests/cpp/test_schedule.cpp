@@ -238,74 +238,6 @@ void check_split(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s) {
   CHECK(s.split_preferred == (units < 160 && longest > 2 * kRowWaves * vbsr_amd::kStepRun));
 }
 
-// rows_tile: one row per workgroup, in rows_wide's order with each packed
-// workgroup's rows at consecutive positions of its XCD; the split
-// schedule's items_tile: every part once, in the order of its items.
-void check_tiles(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s) {
-  using vbsr_amd::kRowWaves;
-  using vbsr_amd::kXcds;
-  CHECK(s.groups_tile % kXcds == 0 && int64_t(s.rows_tile.size()) == s.groups_tile);
-  std::vector<std::vector<int32_t>> expect(kXcds), got(kXcds);
-  for (int64_t g = 0; g < s.groups; ++g)
-    for (int w = 0; w < kRowWaves; ++w) {
-      const auto& item = s.rows_wide[size_t(g) * kRowWaves + size_t(w)];
-      if (item.step_count >= 0 && item.lead == 0) expect[size_t(g % kXcds)].push_back(item.row);
-    }
-  std::vector<int> seen(size_t(m.block_rows), 0);
-  for (int64_t g = 0; g < s.groups_tile; ++g) {
-    const auto& item = s.rows_tile[size_t(g)];
-    if (item.step_count < 0) {
-      CHECK(item.row == -1);
-      continue;
-    }
-    CHECK(item.row >= 0 && item.row < m.block_rows);
-    if (item.row < 0 || item.row >= m.block_rows) continue;
-    ++seen[size_t(item.row)];
-    got[size_t(g % kXcds)].push_back(item.row);
-    CHECK(item.group == 1 && item.lead == 0 && item.h == m.row_size[item.row] &&
-          item.c_off == m.row_scalar_off[item.row]);
-    const bool has = item.step_count > 0;
-    CHECK(item.first.a_off == (has ? s.steps[size_t(item.step_first)].a_off : 0));
-    CHECK(item.first.b_off == (has ? s.steps[size_t(item.step_first)].b_off : 0));
-  }
-  for (int32_t i = 0; i < m.block_rows; ++i) CHECK(seen[size_t(i)] == 1);
-  for (int x = 0; x < kXcds; ++x) CHECK(got[size_t(x)] == expect[size_t(x)]);
-  // Within an XCD's band every real row precedes the padding.
-  for (int x = 0; x < kXcds; ++x) {
-    bool idle_seen = false;
-    for (int64_t g = x; g < s.groups_tile; g += kXcds) {
-      const bool idle = s.rows_tile[size_t(g)].step_count < 0;
-      CHECK(!(idle_seen && !idle));
-      idle_seen = idle_seen || idle;
-    }
-  }
-
-  const auto& sp = s.split;
-  CHECK(sp.groups_tile % kXcds == 0 && int64_t(sp.items_tile.size()) == sp.groups_tile);
-  std::vector<const vbsr_amd::WaveItem*> parts;
-  for (int64_t g = 0; g < sp.groups; ++g) {
-    const auto* wg = &sp.items[size_t(g) * kRowWaves];
-    for (int w = 0; w < kRowWaves; ++w)
-      if (wg[w].step_count >= 0 && wg[w].lead == 0) parts.push_back(&wg[w]);
-  }
-  size_t q = 0;
-  bool idle_seen = false;
-  for (const auto& item : sp.items_tile) {
-    if (item.step_count < 0) {
-      idle_seen = true;
-      continue;
-    }
-    CHECK(!idle_seen && q < parts.size());
-    if (idle_seen || q >= parts.size()) break;
-    const auto& part = *parts[q++];
-    CHECK(item.c_off == part.c_off && item.step_first == part.step_first && item.step_count == part.step_count &&
-          item.h == part.h && item.row == part.row && item.group == 1 && item.lead == 0);
-    const bool has = item.step_count > 0;
-    CHECK(item.first.a_off == (has ? s.steps[size_t(item.step_first)].a_off : 0));
-  }
-  CHECK(q == parts.size());
-}
-
 bool same(const std::vector<vbsr_amd::WaveItem>& a, const std::vector<vbsr_amd::WaveItem>& b) {
   return a.size() == b.size() && (a.empty() || std::memcmp(a.data(), b.data(), a.size() * sizeof(a[0])) == 0);
 }
@@ -324,10 +256,8 @@ void check_view(const vbsr_host_view& m, const char* name, double max_seconds) {
   std::vector<int> xcd_of_row(size_t(m.block_rows), -1);
   check_order(m, s, s.rows, xcd_of_row, false);
   check_order(m, s, s.rows_wide, xcd_of_row, true);
-  check_tiles(m, s);
   const vbsr_amd::HostSchedule again = vbsr_amd::build_schedule(m);
   if (!(same(s.rows, again.rows) && same(s.rows_wide, again.rows_wide) && same(s.split.items, again.split.items) &&
-        same(s.rows_tile, again.rows_tile) && same(s.split.items_tile, again.split.items_tile) &&
         s.steps.size() == again.steps.size())) {
     std::fprintf(stderr, "FAILED: schedule not deterministic\n");
     ++failures;

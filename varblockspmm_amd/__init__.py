@@ -55,8 +55,7 @@ class GeneratorOptions(ctypes.Structure):
 
 class RowSchedule(ctypes.Structure):
     _fields_ = [("steps", ctypes.c_void_p), ("rows", ctypes.c_void_p), ("groups", ctypes.c_int64),
-                ("step_limit", ctypes.c_int32), ("rows_wide", ctypes.c_void_p), ("rows_tile", ctypes.c_void_p),
-                ("groups_tile", ctypes.c_int64)]
+                ("step_limit", ctypes.c_int32), ("rows_wide", ctypes.c_void_p)]
 
 
 class PlanOptions(ctypes.Structure):

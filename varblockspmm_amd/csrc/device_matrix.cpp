@@ -59,14 +59,10 @@ DeviceMatrix::DeviceMatrix(const vbsr_host_view& host) {
     schedule_.rows = upload(schedule.rows.data(), int64_t(schedule.rows.size()), allocations_);
     schedule_.rows_wide = upload(schedule.rows_wide.data(), int64_t(schedule.rows_wide.size()), allocations_);
     schedule_.groups = schedule.groups;
-    schedule_.rows_tile = upload(schedule.rows_tile.data(), int64_t(schedule.rows_tile.size()), allocations_);
-    schedule_.groups_tile = schedule.groups_tile;
     schedule_.step_limit = int32_t(std::max<size_t>(schedule.steps.size(), 1) - 1);
     split_.items = upload(schedule.split.items.data(), int64_t(schedule.split.items.size()), allocations_);
     split_.rows = upload(schedule.split.rows.data(), int64_t(schedule.split.rows.size()), allocations_);
     split_.groups = schedule.split.groups;
-    split_.items_tile = upload(schedule.split.items_tile.data(), int64_t(schedule.split.items_tile.size()), allocations_);
-    split_.groups_tile = schedule.split.groups_tile;
     split_.virtual_rows = schedule.split.virtual_rows;
     split_.preferred = schedule.split_preferred;
   } catch (...) {

@@ -101,8 +101,6 @@ static_assert(sizeof(SplitRowRec) == 32, "SplitRowRec is read as 8 dwords");
 
 struct HostSplitSchedule {
   std::vector<WaveItem> items;     // kRowWaves per workgroup; a part's c_off is its first virtual row
-  std::vector<WaveItem> items_tile;  // one part per workgroup, for the RHS 64 kernel
-  int64_t groups_tile{};             // workgroups of the RHS 64 partial launch (multiple of kXcds)
   std::vector<SplitRowRec> rows;   // one per block row
   int64_t groups{};                // workgroups of the partial launch (multiple of kXcds)
   int64_t virtual_rows{};          // workspace rows: the sum over parts of h
@@ -114,11 +112,6 @@ struct HostSchedule {
   std::vector<WaveItem> rows;       // kRowWaves per workgroup, launch order for RHS 8 and 16
   std::vector<WaveItem> rows_wide;  // the same workgroups, launch order for RHS 32 and 64
   int64_t groups{};                 // workgroups of one launch (multiple of kXcds)
-  // RHS 64's tile-split kernel takes one row per workgroup: the rows_wide
-  // order with each packed workgroup's rows given workgroups of their own,
-  // at consecutive positions on the same XCD.
-  std::vector<WaveItem> rows_tile;
-  int64_t groups_tile{};
   HostSplitSchedule split;
   // Whether Plan's automatic choice takes the split-row path: the row-owned
   // launch would leave most CUs idle while its rows are long.
@@ -149,10 +142,8 @@ public:
   // Device copy of the split-row schedule.
   struct Split {
     const WaveItem* items{};
-    const WaveItem* items_tile{};
     const SplitRowRec* rows{};
     int64_t groups{};
-    int64_t groups_tile{};
     int64_t virtual_rows{};
     bool preferred{};
   };

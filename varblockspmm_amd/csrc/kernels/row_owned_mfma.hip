@@ -12,13 +12,9 @@
 // wave accumulates all T = ceil(h/16) row tiles for its steps.  The four
 // partial slabs of a shared row are summed in LDS in a fixed order,
 // (w0 + w2) + (w1 + w3): at RHS 16 and 32 by wave 0 after one barrier, at
-// RHS 8 (and in the VALU variant at 64) in pairs over three barriers.  A packed row's wave stores its
+// RHS 8 and 64 in pairs over three barriers.  A packed row's wave stores its
 // sums itself.  The accumulation order depends only on the matrix, so
 // results are bit-identical from run to run.
-//
-// At RHS 64 the tile-split kernel (row_tiles_kernel, below) runs instead:
-// one row per workgroup, wave w computing RHS columns 16 w .. 16 w + 15 over
-// all of the row's steps, with each step's A tile shared through LDS.
 //
 // Arithmetic.  v_mfma_f32_16x16x4_f32 on transposed 16x16 output tiles,
 //   D[n][r] = sum_k B[k, n0 + n] * A[16t + r, k],
@@ -510,157 +506,9 @@ __global__ __launch_bounds__(kThreads) void row_owned_mfma_kernel(Launch L) {
   }
 }
 
-// RHS 64: the tile-split kernel.  Wave w owns RHS tile w (C columns
-// 16 w .. 16 w + 15) of the workgroup's row over all of the row's k steps, so
-// the row needs no split-k and no reduction, and a wave holds T accumulator
-// tiles per chain instead of 4 T.  Each step's A tile is loaded once for the
-// four waves: lane i of the workgroup reads floats 4 i .. 4 i + 3 of the
-// step's column-major 16 x h tile (whole lines, non-temporal) into a
-// double-buffered LDS tile, and one barrier per step publishes it; each wave
-// moves its own B tile through its LDS slot as the split-k kernel does.  Step
-// j + 1's loads are in flight while step j computes.  Steps alternate between
-// two accumulator chains (even and odd steps), summed at the end as
-// even + odd, which halves the length of each rounding chain.  It runs one
-// row per workgroup (the schedule's rows_tile order), light rows included:
-// all four waves share even a one-step row.
-//
-// Against the split-k kernel at RHS 64 this frees 48 accumulator registers
-// per wave (6 waves per SIMD instead of 3) and drops the three-barrier
-// reduction: 93.0 against 99.2 us at configuration 3, alternating on one
-// box.  At RHS 32 the same split over two waves is 6% slower than split-k,
-// so RHS 8-32 keep the split-k kernel.
-constexpr int kTileLd = 16 * kMaxTiles + 4;       // A tile: float (r, k) at k * kTileLd + r
-constexpr int kTileFloats = 16 * kTileLd;         // one A buffer
-constexpr int kTileChains = 2;
-constexpr int kTileLdsBytes = 2 * kTileFloats * 4 + kWaves * kWave * 16;
-
-template <int T>
-__device__ __forceinline__ void tile_row(const Launch& L, const WaveItem& item, char* lds, int wave, int lane) {
-  constexpr int ld = kTileLd;
-  const int group = lane >> 4;
-  const int x = lane & 15;
-  const int tid = wave * kWave + lane;
-  const int h = uniform(item.h);
-  const int count = uniform(item.step_count);
-  const int first = uniform(item.step_first);
-  const int last_rows = h - 16 * (T - 1);  // 8 or 16
-  const uint32_t ldb = uint32_t(L.a.scalar_cols);
-  float* a_tiles = reinterpret_cast<float*>(lds);
-  f32x4* b_slot = reinterpret_cast<f32x4*>(lds + 2 * kTileFloats * 4) + wave * kWave;
-
-  // This lane's four floats of the A tile, f = 4 tid .. 4 tid + 3 (one
-  // column: h is a multiple of 8), or the padding rows 64 .. 67 of column
-  // tid & 15 for lanes past the tile.  f / h as in row_body (exact for
-  // f < 1024).
-  const uint32_t h_recip = uint32_t(uniform(int((65536u + uint32_t(h) - 1u) / uint32_t(h))));
-  const int f = 4 * tid;
-  const int fk = int((uint32_t(f) * h_recip) >> 16);
-  const int a_write = f < 16 * h ? fk * ld + (f - fk * h) : (tid & 15) * ld + 16 * kMaxTiles;
-  const int a_read = 4 * group * ld + x;
-  const int a_read_last = 4 * group * ld + 16 * (T - 1) + (x & (last_rows - 1));
-  const uint32_t a_full_bytes = uint32_t(16 * h) * 4u;
-  const uint32_t a_half_bytes = uint32_t(8 * h) * 4u;
-
-  // B tile `wave`: lane 4n + q reads B[k0 + 4q .. k0 + 4q + 3, 16 wave + n].
-  const int b_n = lane >> 2;
-  const int b_q = lane & 3;
-  const uint32_t b_full = uint32_t(b_n) * ldb * 4u + uint32_t(16 * b_q);
-  const uint32_t b_half = b_q < 2 ? b_full : kOutOfRange;
-  const uint32_t b_span = 15u * ldb * 4u;
-  const int slot_write = b_slot_index(b_n, b_q);
-  const int slot_read = b_slot_index(x, group);
-
-  f32x4 acc[kTileChains][T];
-#pragma unroll
-  for (int c = 0; c < kTileChains; ++c)
-#pragma unroll
-    for (int t = 0; t < T; ++t) acc[c][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-  struct TileStage {
-    f32x4 a, b;
-  };
-  for (int seg = 0; seg < count; seg += kWave) {
-    const int seg_count = min(kWave, count - seg);
-    const StepRec rec = L.steps[min(first + seg + min(lane, seg_count - 1), L.step_limit)];
-    auto issue = [&](TileStage& st, int j, bool live) {
-      const int l = min(j, kWave - 1);
-      const bool leading = seg == 0 && j == 0;
-      const int64_t a_off = leading ? item.first.a_off : lane_value(rec.a_off, l);
-      const int64_t b_word = leading ? item.first.b_off : lane_value(rec.b_off, l);
-      const bool half = (b_word & kHalfStep) != 0;
-      const rsrc_t a_rsrc = make_rsrc(L.a.values + a_off, live ? (half ? a_half_bytes : a_full_bytes) : 0u);
-      st.a = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, 16 * tid, 0, kNonTemporal));
-      const uint32_t b_bytes = live ? b_span + (half ? 32u : 64u) : 0u;
-      const rsrc_t b_rsrc = make_rsrc(L.b + (b_word & kOffsetMask) + int64_t(wave) * 16 * ldb, b_bytes);
-      st.b = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, int(half ? b_half : b_full), 0, 0));
-    };
-    // Publishes step j's A tile and B tile, then runs its MFMAs into `chain`.
-    // Buffer j & 1 was last read in step j - 2, which every wave finished
-    // before passing step j - 1's barrier.
-    auto compute = [&](const TileStage& st, int j, f32x4 (&chain)[T]) {
-      float* a = a_tiles + (j & 1) * kTileFloats;
-      *reinterpret_cast<f32x4*>(a + a_write) = st.a;
-      b_slot[slot_write] = st.b;
-      __syncthreads();
-      const f32x4 bv = b_slot[slot_read];
-#pragma unroll
-      for (int t = 0; t < T; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float av = t < T - 1 ? a[a_read + 16 * t + i * ld] : a[a_read_last + i * ld];
-          chain[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[i], av, chain[t], 0, 0, 0);
-        }
-    };
-    // Segments hold an even number of steps (64) except the row's last, so
-    // the step's parity picks the chain; a dead odd step multiplies zeros.
-    TileStage r0, r1;
-    issue(r0, 0, true);
-    for (int j = 0; j < seg_count; j += 2) {
-      issue(r1, j + 1, j + 1 < seg_count);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(r0, j, acc[0]);
-      issue(r0, j + 2, j + 2 < seg_count);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(r1, j + 1, acc[1]);
-    }
-    // The next segment's (or row's) first writes must not overtake this
-    // segment's last reads.
-    __syncthreads();
-  }
-
-  const int64_t ldc = L.ldc;
-  float* c_row = L.c + item.c_off + x;
-#pragma unroll
-  for (int t = 0; t < T; ++t) {
-    const f32x4 sum = acc[0][t] + acc[1][t];
-    if (t < T - 1 || x < last_rows) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v) c_row[16 * t + int64_t(wave * 16 + 4 * group + v) * ldc] = sum[v];
-    }
-  }
-}
-
-// One workgroup per item (L.items holds one item per workgroup here).
-__global__ __launch_bounds__(kThreads) void row_tiles_kernel(Launch L) {
-  __shared__ __attribute__((aligned(16))) char lds[kTileLdsBytes];
-  const int wave = uniform(int(threadIdx.x) / kWave);
-  const int lane = int(threadIdx.x) % kWave;
-  const WaveItem item = L.items[blockIdx.x];
-  if (uniform(item.step_count) < 0) return;  // padding: the whole workgroup leaves
-  switch ((uniform(item.h) + 15) >> 4) {
-  case 1: tile_row<1>(L, item, lds, wave, lane); break;
-  case 2: tile_row<2>(L, item, lds, wave, lane); break;
-  case 3: tile_row<3>(L, item, lds, wave, lane); break;
-  default: tile_row<4>(L, item, lds, wave, lane); break;
-  }
-}
-
 template <int RHS, bool kValu>
 void launch(const Launch& L, int64_t groups, hipStream_t stream) {
-  if constexpr (RHS == 64 && !kValu)
-    row_tiles_kernel<<<dim3(unsigned(groups)), dim3(kThreads), 0, stream>>>(L);
-  else
-    row_owned_mfma_kernel<RHS, kValu><<<dim3(unsigned(groups)), dim3(kThreads), 0, stream>>>(L);
+  row_owned_mfma_kernel<RHS, kValu><<<dim3(unsigned(groups)), dim3(kThreads), 0, stream>>>(L);
 }
 
 template <bool kValu>
@@ -755,14 +603,10 @@ void launch_row_owned_math(const vbsr_device_view& a, const vbsr_row_schedule& s
   if (!row_owned_supported(a, b, c, rhs))
     throw std::invalid_argument(
         "row-owned kernel needs (min(rhs, 16) - 1) * K * 4 + 128 <= 0xfffffff0 (its 32-bit B offsets)");
-  // RHS 64's MFMA kernel runs one row per workgroup (rows_tile); the
-  // split-k kernels run the four-item workgroups of rows or rows_wide.
-  const bool tiles = rhs == 64 && !kValu;
-  if (tiles && s.rows_tile == nullptr && s.groups_tile > 0) throw std::invalid_argument("schedule without rows_tile");
-  const void* rows = tiles ? s.rows_tile : rhs >= 32 && s.rows_wide != nullptr ? s.rows_wide : s.rows;
+  const void* rows = rhs >= 32 && s.rows_wide != nullptr ? s.rows_wide : s.rows;
   const Launch L{a, static_cast<const StepRec*>(s.steps), static_cast<const WaveItem*>(rows), s.step_limit, b, c,
                  a.scalar_rows};
-  launch_items<kValu>(L, tiles ? s.groups_tile : s.groups, rhs, stream);
+  launch_items<kValu>(L, s.groups, rhs, stream);
 }
 
 }  // namespace
@@ -796,10 +640,9 @@ void launch_split_row(const vbsr_device_view& a, const vbsr_row_schedule& s, con
     check_panels(split.virtual_rows, a.scalar_rows, c, workspace, rhs);
   }
   if (a.block_rows <= 0) return;
-  const bool tiles = rhs == 64;  // one part per workgroup for the RHS 64 kernel
-  const Launch L{a, static_cast<const StepRec*>(s.steps), tiles ? split.items_tile : split.items, s.step_limit, b,
-                 workspace, split.virtual_rows};
-  launch_items<false>(L, tiles ? split.groups_tile : split.groups, rhs, stream);
+  const Launch L{a, static_cast<const StepRec*>(s.steps), split.items, s.step_limit, b, workspace,
+                 split.virtual_rows};
+  launch_items<false>(L, split.groups, rhs, stream);
   // A row's slab holds at most 64 * rhs elements.
   const unsigned chunks = unsigned((64 * rhs + kReduceThreads - 1) / kReduceThreads);
   split_reduce_kernel<<<dim3(unsigned(a.block_rows), chunks), dim3(kReduceThreads), 0, stream>>>(

@@ -223,39 +223,6 @@ HostSchedule build_schedule(const vbsr_host_view& m) {
   }
   emit(chained, out.rows_wide);
 
-  // The same order with one row per workgroup, for the RHS 64 kernel: a
-  // packed workgroup's rows get consecutive positions on its XCD.
-  auto row_item = [&](int32_t i) {
-    WaveItem item{};
-    item.c_off = m.row_scalar_off[i];
-    item.step_first = step_first[size_t(i)];
-    item.step_count = steps_of(i);
-    item.h = m.row_size[i];
-    item.row = i;
-    item.group = 1;
-    item.lead = 0;
-    if (item.step_count > 0) item.first = out.steps[size_t(item.step_first)];
-    return item;
-  };
-  {
-    std::vector<std::vector<int32_t>> tile_bands(kXcds);
-    size_t per = 0;
-    for (int xcd = 0; xcd < kXcds; ++xcd) {
-      for (const size_t u : chained[size_t(xcd)])
-        for (const int32_t i : units[u]) tile_bands[size_t(xcd)].push_back(i);
-      per = std::max(per, tile_bands[size_t(xcd)].size());
-    }
-    out.groups_tile = int64_t(per) * kXcds;
-    WaveItem idle{};
-    idle.step_count = -1;
-    idle.row = -1;
-    idle.group = 1;
-    out.rows_tile.assign(size_t(out.groups_tile), idle);
-    for (int xcd = 0; xcd < kXcds; ++xcd)
-      for (size_t pos = 0; pos < tile_bands[size_t(xcd)].size(); ++pos)
-        out.rows_tile[pos * kXcds + size_t(xcd)] = row_item(tile_bands[size_t(xcd)][pos]);
-  }
-
   // Split-row schedule.  Parts of a row hold part_steps consecutive steps (a
   // multiple of one run per wave, sized so that the parts of the whole
   // matrix fill about kSplitTargetGroups workgroups); the row's last part
@@ -337,28 +304,6 @@ HostSchedule build_schedule(const vbsr_host_view& m) {
       if (first < item.step_count) item.first = out.steps[size_t(item.step_first + first)];
     }
   }
-  // One part per workgroup for the RHS 64 kernel, in the same order.
-  {
-    std::vector<WaveItem> list;
-    for (const auto& unit : split_units)
-      for (const size_t q : unit) {
-        const Part& p = parts[q];
-        WaveItem item{};
-        item.c_off = p.w_off;
-        item.step_first = p.step_first;
-        item.step_count = p.step_count;
-        item.h = m.row_size[p.row];
-        item.row = p.row;
-        item.group = 1;
-        item.lead = 0;
-        if (item.step_count > 0) item.first = out.steps[size_t(item.step_first)];
-        list.push_back(item);
-      }
-    sp.groups_tile = int64_t((list.size() + kXcds - 1) / kXcds) * kXcds;
-    list.resize(size_t(sp.groups_tile), idle);
-    sp.items_tile = std::move(list);
-  }
-
   // Automatic choice: the row-owned launch would occupy fewer than 160 of
   // the 256 CUs, and its longest row needs three or more runs per wave.
   // Measured at degree 16 (high sizes, random columns): the split-row path
