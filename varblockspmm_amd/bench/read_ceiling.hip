@@ -13,6 +13,11 @@
 //             it.
 //   l2        16 MiB read 8 times per launch: each XCD's eighth (2 MiB) stays
 //             in its L2.
+//   dram_regions_48k / _8k
+//             168 MiB (A at configuration 3) read once, cold, laid out as the
+//             row-owned kernel reads A: one workgroup per contiguous 48 KiB
+//             (about a block row's A) or 8 KiB region, which it reads and
+//             leaves.
 // Each case runs with plain and with non-temporal 16-byte loads.
 //
 // Workgroup i runs on XCD i mod 8; the grid is a multiple of 8 and each
@@ -69,16 +74,49 @@ __global__ __launch_bounds__(kThreads) void read_kernel(const f32x4* __restrict_
   if (total != 0.0f) sink[blockIdx.x * kThreads + threadIdx.x] = total;
 }
 
+// The same reads laid out as the row-owned kernel reads A: workgroup b reads
+// only its own contiguous region of `region` vectors (a block row's A), its
+// four waves taking interleaved 1 KB pieces, kUnroll in flight per lane, and
+// leaves; the grid covers the buffer once.
+template <bool kNonTemporal>
+__global__ __launch_bounds__(kThreads) void region_kernel(const f32x4* __restrict__ data, int64_t region,
+                                                          float* __restrict__ sink) {
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const f32x4* base = data + int64_t(blockIdx.x) * region;
+  const int64_t chunk = int64_t(kThreads) * kUnroll;
+  for (int64_t i0 = threadIdx.x; i0 < region; i0 += chunk) {
+    f32x4 v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = i0 + int64_t(u) * kThreads;
+      if (i < region)
+        v[u] = kNonTemporal ? __builtin_nontemporal_load(base + i) : base[i];
+      else
+        v[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) acc += v[u];
+  }
+  const float total = acc.x + acc.y + acc.z + acc.w;
+  if (total != 0.0f) sink[threadIdx.x] = total;
+}
+
 struct Result {
   double median_us, gbps;
 };
 
+// region_bytes == 0: the strided sweep (read_kernel); otherwise one
+// workgroup per region of that many bytes (region_kernel, one pass).
 template <bool kNonTemporal>
 Result run(const float* buffer, int64_t bytes, int passes, const float* flush, int64_t flush_bytes, int reps,
-           int grid, float* sink, hipStream_t stream) {
+           int grid, float* sink, hipStream_t stream, int64_t region_bytes = 0) {
   const int64_t count = bytes / 16;
   const auto launch = [&](const float* p, int64_t n, int k) {
-    read_kernel<kNonTemporal><<<grid, kThreads, 0, stream>>>(reinterpret_cast<const f32x4*>(p), n, k, sink);
+    if (region_bytes > 0 && p == buffer)
+      region_kernel<kNonTemporal><<<unsigned(n / (region_bytes / 16)), kThreads, 0, stream>>>(
+          reinterpret_cast<const f32x4*>(p), region_bytes / 16, sink);
+    else
+      read_kernel<kNonTemporal><<<grid, kThreads, 0, stream>>>(reinterpret_cast<const f32x4*>(p), n, k, sink);
   };
   hipEvent_t start, stop;
   check(hipEventCreateWithFlags(&start, hipEventDisableSystemFence), "hipEventCreate");
@@ -130,18 +168,24 @@ int main(int argc, char** argv) {
     int64_t bytes;
     int passes;
     bool flushed;
+    int64_t region;  // bytes per workgroup (0: strided sweep)
   };
-  const Case cases[] = {{"dram", GiB, 1, true}, {"mall", 96 * MiB, 4, false}, {"l2", 16 * MiB, 8, false}};
+  const Case cases[] = {{"dram", GiB, 1, true, 0},
+                        {"mall", 96 * MiB, 4, false, 0},
+                        {"l2", 16 * MiB, 8, false, 0},
+                        {"dram_regions_48k", 168 * MiB, 1, true, 48 * 1024},
+                        {"dram_regions_8k", 168 * MiB, 1, true, 8 * 1024}};
   for (const Case& c : cases) {
     for (const bool nt : {false, true}) {
       const Result r = nt ? run<true>(dram, c.bytes, c.passes, c.flushed ? flush : nullptr, GiB, reps, grid, sink,
-                                      stream)
+                                      stream, c.region)
                           : run<false>(dram, c.bytes, c.passes, c.flushed ? flush : nullptr, GiB, reps, grid, sink,
-                                       stream);
+                                       stream, c.region);
+      const int launched = c.region > 0 ? int(c.bytes / c.region) : grid;
       std::printf("{\"case\": \"%s\", \"loads\": \"%s\", \"bytes_per_pass\": %lld, \"passes\": %d, \"median_us\": "
                   "%.2f, \"GB_per_s\": %.1f, \"grid\": %d, \"reps\": %d}\n",
                   c.name, nt ? "nontemporal" : "plain", static_cast<long long>(c.bytes), c.passes, r.median_us,
-                  r.gbps, grid, reps);
+                  r.gbps, launched, reps);
       std::fflush(stdout);
     }
   }
