@@ -856,13 +856,16 @@ def test_concurrent_executes_on_two_streams():
         matrix.close()
 
 
-def test_plan_execute_replays_from_a_hip_graph():
-    """execute enqueues one kernel and allocates nothing, so it can be captured into a HIP graph;
-    every replay, with eager work and synchronisations between replays, equals the eager result."""
+@pytest.mark.parametrize("kernel", ["auto", "split_row"])
+def test_plan_execute_replays_from_a_hip_graph(kernel):
+    """execute enqueues its kernels (one, or two on the split-row path, which uses the plan's own
+    workspace) and allocates nothing, so it can be captured into a HIP graph; every replay, with eager
+    work and synchronisations between replays, equals the eager result."""
     host = vb.generate(256, 256, 8, "high", "random", 41)
     c = Case(host, 32, 41)
     try:
-        plan = vb.Plan(c.matrix, 32)
+        plan = vb.Plan(c.matrix, 32, kernel)
+        assert plan.launch_count() == (2 if kernel == "split_row" else 1)
         eager = c.run_plan(plan)
         c.check_tolerance(eager, "eager")
         capture_stream = torch.cuda.Stream(device=DEVICE)
