@@ -9,8 +9,10 @@
 //     first step record;
 //   * both orders place each row on the same XCD (workgroup index mod 8), and
 //     no XCD's work exceeds an eighth of the total by more than one row's;
-//   * `rows` runs each XCD's workgroups heaviest first; `rows_wide` ends each
-//     XCD's band with its lightest quarter, heaviest first;
+//   * `rows` runs each XCD's workgroups heaviest first; `rows_wide` chains
+//     only shared workgroups of the heavier three quarters and ends each
+//     XCD's band with the rest (packed workgroups and the lightest quarter),
+//     heaviest first;
 //   * the split-row schedule: each row's parts cover its steps in order and
 //     take consecutive virtual rows, every part is in exactly one workgroup,
 //     and the automatic choice follows its rule;
@@ -62,6 +64,7 @@ void check_order(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s,
   std::vector<int> seen(size_t(m.block_rows), 0);
   std::vector<int64_t> load(kXcds, 0);
   std::vector<std::vector<int64_t>> band_work(kXcds);
+  std::vector<std::vector<char>> band_shared(kXcds);
   bool padding_started[kXcds] = {};
   for (int64_t g = 0; g < s.groups; ++g) {
     const auto* wg = &items[size_t(g) * kRowWaves];
@@ -108,6 +111,7 @@ void check_order(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s,
     }
     load[size_t(xcd)] += work;
     band_work[size_t(xcd)].push_back(work);
+    band_shared[size_t(xcd)].push_back(shared ? 1 : 0);
   }
   for (int32_t i = 0; i < m.block_rows; ++i) CHECK(seen[size_t(i)] == 1);
   int64_t heaviest = 0;
@@ -118,13 +122,24 @@ void check_order(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s,
   int64_t total = 0;
   for (const int64_t l : load) total += l;
   CHECK(*std::max_element(load.begin(), load.end()) <= total / kXcds + 1 + heaviest);
-  for (const auto& band : band_work) {
-    const size_t tail = wide ? band.size() / 4 : band.size();
-    const size_t from = band.size() - tail;
+  for (int x = 0; x < kXcds; ++x) {
+    const auto& band = band_work[size_t(x)];
+    // rows_wide: only shared workgroups are chained; the first packed one
+    // (or the lightest quarter, whichever comes first) starts a tail that
+    // runs heaviest first to the end.
+    size_t from = wide ? band.size() - band.size() / 4 : 0;
+    if (wide)
+      for (size_t q = 0; q < from; ++q)
+        if (!band_shared[size_t(x)][q]) {
+          from = q;
+          break;
+        }
     for (size_t q = from + 1; q < band.size(); ++q) CHECK(band[q - 1] >= band[q]);
-    if (wide && tail > 0) {
-      const int64_t tail_max = *std::max_element(band.begin() + std::ptrdiff_t(from), band.end());
-      for (size_t q = 0; q < from; ++q) CHECK(band[q] >= tail_max);
+    // The lightest quarter comes last: nothing before it is lighter.
+    const size_t light = band.size() - band.size() / 4;
+    if (wide && light < band.size()) {
+      const int64_t light_max = *std::max_element(band.begin() + std::ptrdiff_t(light), band.end());
+      for (size_t q = 0; q < light; ++q) CHECK(band[q] >= light_max);
     }
   }
 }
@@ -353,6 +368,8 @@ int main() {
       {1024, 1024, 8, VBSR_DIST_LOW_VARIANCE, VBSR_LOCALITY_RANDOM},
       {4096, 4096, 16, VBSR_DIST_BIMODAL, VBSR_LOCALITY_RANDOM},
       {4096, 4096, 1, VBSR_DIST_UNIFORM, VBSR_LOCALITY_RANDOM},
+      {4096, 4096, 1, VBSR_DIST_HIGH_VARIANCE, VBSR_LOCALITY_RANDOM},
+      {2048, 2048, 2, VBSR_DIST_HIGH_VARIANCE, VBSR_LOCALITY_LOCAL_CLAMPED},
       {9, 17, 4, VBSR_DIST_HIGH_VARIANCE, VBSR_LOCALITY_LOCAL},
       {5, 3, 2, VBSR_DIST_BIMODAL, VBSR_LOCALITY_RANDOM},
       {1, 1, 1, VBSR_DIST_UNIFORM, VBSR_LOCALITY_RANDOM},

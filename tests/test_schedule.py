@@ -19,7 +19,7 @@ def test_schedule_program():
     print(result.stdout)
     assert result.returncode == 0, result.stdout + result.stderr
     assert result.stdout.strip().endswith("ALL OK")
-    assert result.stdout.count("\nok ") + result.stdout.startswith("ok ") == 14
+    assert result.stdout.count("\nok ") + result.stdout.startswith("ok ") == 16
 
 
 def test_validate_fuzz_program():
