@@ -190,7 +190,7 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the VBSR SpMM path has no multi-GPU code "
-              "(row sharding plus a B broadcast is described in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "(it would shard by block rows, with B broadcast to every GPU). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
