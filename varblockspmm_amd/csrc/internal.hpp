@@ -70,8 +70,7 @@ constexpr int kPackSteps = 4;
 // a padding workgroup) has step_count < 0.  `first` repeats the wave's first
 // step record (zero when it has none), so the kernel can issue that step's
 // loads as soon as the item arrives instead of after the step records.
-// 48 bytes, read with scalar loads; a workgroup's kRowWaves items are
-// consecutive.
+// 48 bytes; a workgroup's kRowWaves items are consecutive.
 struct alignas(16) WaveItem {
   int64_t c_off;       // row_scalar_off[row]: first row of C written
   int32_t step_first;  // index of the row's first StepRec
