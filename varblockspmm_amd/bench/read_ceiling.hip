@@ -19,6 +19,13 @@
 //             (about a block row's A) or 8 KiB region, which it reads and
 //             leaves.
 // Each case runs with plain and with non-temporal 16-byte loads.
+//   mixed     the row-owned kernel's mix of L2 misses at configuration 3
+//             (about equal bytes of each): one launch reads 168 MiB once,
+//             cold, with non-temporal loads (as it reads A) and, interleaved
+//             with those, an 84 MiB buffer twice with plain loads, which the
+//             Infinity Cache holds and each XCD's L2 does not (as it reads
+//             B's line misses).  The Infinity Cache buffer is read once before
+//             each timed launch, after the flush.
 //
 // Workgroup i runs on XCD i mod 8; the grid is a multiple of 8 and each
 // workgroup reads 16 KiB chunks i, i + grid, ..., so each XCD reads one
@@ -101,6 +108,31 @@ __global__ __launch_bounds__(kThreads) void region_kernel(const f32x4* __restric
   if (total != 0.0f) sink[threadIdx.x] = total;
 }
 
+// The mixed case: lane loads alternate between `cold` (non-temporal, read
+// once) and `warm` (plain; index i mod warm_count, so it is swept
+// cold_count / warm_count times), kUnroll of each in flight.
+__global__ __launch_bounds__(kThreads) void mixed_kernel(const f32x4* __restrict__ cold, int64_t cold_count,
+                                                         const f32x4* __restrict__ warm, int64_t warm_count,
+                                                         float* __restrict__ sink) {
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int64_t chunk = int64_t(kThreads) * kUnroll;
+  const int64_t stride = int64_t(gridDim.x) * chunk;
+  for (int64_t base = int64_t(blockIdx.x) * chunk + threadIdx.x; base < cold_count; base += stride) {
+    f32x4 v[2 * kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + int64_t(u) * kThreads;
+      const bool in = i < cold_count;
+      v[2 * u] = in ? __builtin_nontemporal_load(cold + i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      v[2 * u + 1] = in ? warm[i % warm_count] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int u = 0; u < 2 * kUnroll; ++u) acc += v[u];
+  }
+  const float total = acc.x + acc.y + acc.z + acc.w;
+  if (total != 0.0f) sink[blockIdx.x * kThreads + threadIdx.x] = total;
+}
+
 struct Result {
   double median_us, gbps;
 };
@@ -140,6 +172,34 @@ Result run(const float* buffer, int64_t bytes, int passes, const float* flush, i
   check(hipEventDestroy(start), "destroy");
   check(hipEventDestroy(stop), "destroy");
   return {median, double(bytes) * passes / (median * 1e3)};
+}
+
+Result run_mixed(const float* cold, int64_t cold_bytes, const float* warm, int64_t warm_bytes, const float* flush,
+                 int64_t flush_bytes, int reps, int grid, float* sink, hipStream_t stream) {
+  hipEvent_t start, stop;
+  check(hipEventCreateWithFlags(&start, hipEventDisableSystemFence), "hipEventCreate");
+  check(hipEventCreateWithFlags(&stop, hipEventDisableSystemFence), "hipEventCreate");
+  std::vector<double> us;
+  for (int r = 0; r < reps + 1; ++r) {  // the first launch is a warm-up
+    // Plain reads allocate in L2 and the Infinity Cache, so the flush
+    // evicts the cold buffer from both; then the warm buffer is loaded.
+    read_kernel<false><<<grid, kThreads, 0, stream>>>(reinterpret_cast<const f32x4*>(flush), flush_bytes / 16, 1, sink);
+    read_kernel<false><<<grid, kThreads, 0, stream>>>(reinterpret_cast<const f32x4*>(warm), warm_bytes / 16, 1, sink);
+    check(hipEventRecord(start, stream), "record");
+    mixed_kernel<<<grid, kThreads, 0, stream>>>(reinterpret_cast<const f32x4*>(cold), cold_bytes / 16,
+                                                reinterpret_cast<const f32x4*>(warm), warm_bytes / 16, sink);
+    check(hipEventRecord(stop, stream), "record");
+    check(hipEventSynchronize(stop), "sync");
+    float ms = 0;
+    check(hipEventElapsedTime(&ms, start, stop), "elapsed");
+    if (r > 0) us.push_back(double(ms) * 1000.0);
+  }
+  check(hipGetLastError(), "launch");
+  std::sort(us.begin(), us.end());
+  const double median = us[us.size() / 2];
+  check(hipEventDestroy(start), "destroy");
+  check(hipEventDestroy(stop), "destroy");
+  return {median, double(2 * cold_bytes) / (median * 1e3)};
 }
 
 }  // namespace
@@ -188,6 +248,18 @@ int main(int argc, char** argv) {
                   r.gbps, launched, reps);
       std::fflush(stdout);
     }
+  }
+  {
+    // The mixed case reads the first 168 MiB of `dram` cold and the last
+    // 84 MiB of `flush` warm (the rest of `flush` is the flush); it counts
+    // 2 x 168 MiB per launch.
+    const int64_t cold_bytes = 168 * MiB, warm_bytes = 84 * MiB;
+    const Result r = run_mixed(dram, cold_bytes, flush + (GiB - warm_bytes) / 4, warm_bytes, flush, GiB - warm_bytes,
+                               reps, grid, sink, stream);
+    std::printf("{\"case\": \"mixed\", \"loads\": \"nontemporal cold + plain warm\", \"bytes_per_pass\": %lld, "
+                "\"passes\": 1, \"median_us\": %.2f, \"GB_per_s\": %.1f, \"grid\": %d, \"reps\": %d}\n",
+                static_cast<long long>(2 * cold_bytes), r.median_us, r.gbps, grid, reps);
+    std::fflush(stdout);
   }
   check(hipStreamDestroy(stream), "hipStreamDestroy");
   check(hipFree(dram), "hipFree");
