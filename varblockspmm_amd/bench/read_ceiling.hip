@@ -26,6 +26,13 @@
 //             Infinity Cache holds and each XCD's L2 does not (as it reads
 //             B's line misses).  The Infinity Cache buffer is read once before
 //             each timed launch, after the flush.
+//   mixed_segments
+//             the same, with the warm reads shaped as the kernel's B loads:
+//             a K x 32 column-major panel (K = 145,304, as at configuration
+//             3), read in k steps of 16 rows at pseudo-random 8-row
+//             offsets, four lanes per column and 16 columns per load, so
+//             each load reads sixteen 64-byte segments that straddle
+//             128-byte lines as B's do.
 //
 // Workgroup i runs on XCD i mod 8; the grid is a multiple of 8 and each
 // workgroup reads 16 KiB chunks i, i + grid, ..., so each XCD reads one
@@ -133,6 +140,40 @@ __global__ __launch_bounds__(kThreads) void mixed_kernel(const f32x4* __restrict
   if (total != 0.0f) sink[blockIdx.x * kThreads + threadIdx.x] = total;
 }
 
+// mixed_segments: lane loads alternate between `cold` (non-temporal, read
+// once, contiguous) and the panel `b` (plain): load u of a lane reads
+// B[k0 + 4 q .. k0 + 4 q + 3, n] with n = (lane / 4) + 16 (u % 2), q = lane % 4
+// and k0 a pseudo-random multiple of 8 per (iteration, u / 2).
+__global__ __launch_bounds__(kThreads) void mixed_segments_kernel(const f32x4* __restrict__ cold, int64_t cold_count,
+                                                                  const float* __restrict__ b, int64_t k_rows,
+                                                                  float* __restrict__ sink) {
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int64_t chunk = int64_t(kThreads) * kUnroll;
+  const int64_t stride = int64_t(gridDim.x) * chunk;
+  const int lane = int(threadIdx.x) % 64;
+  const int64_t steps = (k_rows - 16) / 8;
+  for (int64_t base = int64_t(blockIdx.x) * chunk + threadIdx.x; base < cold_count; base += stride) {
+    f32x4 v[2 * kUnroll];
+    const uint64_t it = uint64_t(base / chunk);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + int64_t(u) * kThreads;
+      const bool in = i < cold_count;
+      v[2 * u] = in ? __builtin_nontemporal_load(cold + i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      const uint64_t h = (it * 2654435761u + uint64_t(threadIdx.x / 64) * 40503u + uint64_t(u / 2) * 977u) % uint64_t(steps);
+      const int64_t k0 = int64_t(h) * 8;
+      const int64_t n = (lane >> 2) + 16 * (u & 1);
+      const float* p = b + n * k_rows + k0 + 4 * (lane & 3);
+      // p is 16-byte aligned: K, k0 and 4 q are multiples of 4 floats.
+      v[2 * u + 1] = in ? *reinterpret_cast<const f32x4*>(p) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int u = 0; u < 2 * kUnroll; ++u) acc += v[u];
+  }
+  const float total = acc.x + acc.y + acc.z + acc.w;
+  if (total != 0.0f) sink[blockIdx.x * kThreads + threadIdx.x] = total;
+}
+
 struct Result {
   double median_us, gbps;
 };
@@ -174,8 +215,11 @@ Result run(const float* buffer, int64_t bytes, int passes, const float* flush, i
   return {median, double(bytes) * passes / (median * 1e3)};
 }
 
+// segments_k > 0: the warm reads are mixed_segments_kernel's B-shaped
+// segments of a segments_k x 32 panel at `warm`; the bytes counted are then
+// the cold bytes plus the same number of warm bytes requested.
 Result run_mixed(const float* cold, int64_t cold_bytes, const float* warm, int64_t warm_bytes, const float* flush,
-                 int64_t flush_bytes, int reps, int grid, float* sink, hipStream_t stream) {
+                 int64_t flush_bytes, int reps, int grid, float* sink, hipStream_t stream, int64_t segments_k = 0) {
   hipEvent_t start, stop;
   check(hipEventCreateWithFlags(&start, hipEventDisableSystemFence), "hipEventCreate");
   check(hipEventCreateWithFlags(&stop, hipEventDisableSystemFence), "hipEventCreate");
@@ -186,8 +230,12 @@ Result run_mixed(const float* cold, int64_t cold_bytes, const float* warm, int64
     read_kernel<false><<<grid, kThreads, 0, stream>>>(reinterpret_cast<const f32x4*>(flush), flush_bytes / 16, 1, sink);
     read_kernel<false><<<grid, kThreads, 0, stream>>>(reinterpret_cast<const f32x4*>(warm), warm_bytes / 16, 1, sink);
     check(hipEventRecord(start, stream), "record");
-    mixed_kernel<<<grid, kThreads, 0, stream>>>(reinterpret_cast<const f32x4*>(cold), cold_bytes / 16,
-                                                reinterpret_cast<const f32x4*>(warm), warm_bytes / 16, sink);
+    if (segments_k > 0)
+      mixed_segments_kernel<<<grid, kThreads, 0, stream>>>(reinterpret_cast<const f32x4*>(cold), cold_bytes / 16, warm,
+                                                           segments_k, sink);
+    else
+      mixed_kernel<<<grid, kThreads, 0, stream>>>(reinterpret_cast<const f32x4*>(cold), cold_bytes / 16,
+                                                  reinterpret_cast<const f32x4*>(warm), warm_bytes / 16, sink);
     check(hipEventRecord(stop, stream), "record");
     check(hipEventSynchronize(stop), "sync");
     float ms = 0;
@@ -259,6 +307,15 @@ int main(int argc, char** argv) {
     std::printf("{\"case\": \"mixed\", \"loads\": \"nontemporal cold + plain warm\", \"bytes_per_pass\": %lld, "
                 "\"passes\": 1, \"median_us\": %.2f, \"GB_per_s\": %.1f, \"grid\": %d, \"reps\": %d}\n",
                 static_cast<long long>(2 * cold_bytes), r.median_us, r.gbps, grid, reps);
+    std::fflush(stdout);
+    // B-shaped warm reads: a 145,304 x 32 panel (18.6 MB) at the end of `flush`.
+    const int64_t k_rows = 145304, panel_bytes = k_rows * 32 * 4;
+    const Result s = run_mixed(dram, cold_bytes, flush + (GiB - panel_bytes) / 4, panel_bytes, flush,
+                               GiB - panel_bytes - 4096, reps, grid, sink, stream, k_rows);
+    std::printf("{\"case\": \"mixed_segments\", \"loads\": \"nontemporal cold + plain 64-byte B segments\", "
+                "\"bytes_per_pass\": %lld, \"passes\": 1, \"median_us\": %.2f, \"GB_per_s\": %.1f, \"grid\": %d, "
+                "\"reps\": %d}\n",
+                static_cast<long long>(2 * cold_bytes), s.median_us, s.gbps, grid, reps);
     std::fflush(stdout);
   }
   check(hipStreamDestroy(stream), "hipStreamDestroy");
