@@ -9,10 +9,10 @@
 //     first step record;
 //   * both orders place each row on the same XCD (workgroup index mod 8), and
 //     no XCD's work exceeds an eighth of the total by more than one row's;
-//   * `rows` runs each XCD's workgroups heaviest first; `rows_wide` chains
-//     only shared workgroups of the heavier three quarters and ends each
-//     XCD's band with the rest (packed workgroups and the lightest quarter),
-//     heaviest first;
+//   * `rows` runs each XCD's workgroups heaviest first; `rows_wide`, for a
+//     matrix of more than 192 workgroups per XCD, chains the heavier three
+//     quarters of each XCD's band and ends it with the lightest quarter,
+//     heaviest first, and is heaviest first throughout otherwise;
 //   * the split-row schedule: each row's parts cover its steps in order and
 //     take consecutive virtual rows, every part is in exactly one workgroup,
 //     and the automatic choice follows its rule;
@@ -64,7 +64,6 @@ void check_order(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s,
   std::vector<int> seen(size_t(m.block_rows), 0);
   std::vector<int64_t> load(kXcds, 0);
   std::vector<std::vector<int64_t>> band_work(kXcds);
-  std::vector<std::vector<char>> band_shared(kXcds);
   bool padding_started[kXcds] = {};
   for (int64_t g = 0; g < s.groups; ++g) {
     const auto* wg = &items[size_t(g) * kRowWaves];
@@ -111,7 +110,6 @@ void check_order(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s,
     }
     load[size_t(xcd)] += work;
     band_work[size_t(xcd)].push_back(work);
-    band_shared[size_t(xcd)].push_back(shared ? 1 : 0);
   }
   for (int32_t i = 0; i < m.block_rows; ++i) CHECK(seen[size_t(i)] == 1);
   int64_t heaviest = 0;
@@ -122,22 +120,18 @@ void check_order(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s,
   int64_t total = 0;
   for (const int64_t l : load) total += l;
   CHECK(*std::max_element(load.begin(), load.end()) <= total / kXcds + 1 + heaviest);
+  size_t units = 0;
+  for (const auto& band : band_work) units += band.size();
+  const bool chained = wide && units > size_t(kXcds) * 192;
   for (int x = 0; x < kXcds; ++x) {
     const auto& band = band_work[size_t(x)];
-    // rows_wide: only shared workgroups are chained; the first packed one
-    // (or the lightest quarter, whichever comes first) starts a tail that
-    // runs heaviest first to the end.
-    size_t from = wide ? band.size() - band.size() / 4 : 0;
-    if (wide)
-      for (size_t q = 0; q < from; ++q)
-        if (!band_shared[size_t(x)][q]) {
-          from = q;
-          break;
-        }
+    // rows_wide, chained: the heavier three quarters in chain order, then
+    // the lightest quarter heaviest first; otherwise heaviest first.
+    const size_t light = band.size() - band.size() / 4;
+    const size_t from = chained ? light : 0;
     for (size_t q = from + 1; q < band.size(); ++q) CHECK(band[q - 1] >= band[q]);
     // The lightest quarter comes last: nothing before it is lighter.
-    const size_t light = band.size() - band.size() / 4;
-    if (wide && light < band.size()) {
+    if (chained && light < band.size()) {
       const int64_t light_max = *std::max_element(band.begin() + std::ptrdiff_t(light), band.end());
       for (size_t q = 0; q < light; ++q) CHECK(band[q] >= light_max);
     }
@@ -257,7 +251,9 @@ bool same(const std::vector<vbsr_amd::WaveItem>& a, const std::vector<vbsr_amd::
   return a.size() == b.size() && (a.empty() || std::memcmp(a.data(), b.data(), a.size() * sizeof(a[0])) == 0);
 }
 
-void check_view(const vbsr_host_view& m, const char* name, double max_seconds) {
+// reorders: the matrix is random enough that a chained order must differ
+// from the heaviest-first one.
+void check_view(const vbsr_host_view& m, const char* name, double max_seconds, bool reorders = false) {
   const int before = failures;
   const auto t0 = std::chrono::steady_clock::now();
   const vbsr_amd::HostSchedule s = vbsr_amd::build_schedule(m);
@@ -271,6 +267,15 @@ void check_view(const vbsr_host_view& m, const char* name, double max_seconds) {
   std::vector<int> xcd_of_row(size_t(m.block_rows), -1);
   check_order(m, s, s.rows, xcd_of_row, false);
   check_order(m, s, s.rows_wide, xcd_of_row, true);
+  // Up to 192 workgroups per XCD the wide order is the heaviest-first one;
+  // above it, on a random matrix, the chain reorders them.
+  int64_t units = 0;
+  for (size_t g = 0; g < s.rows.size(); g += vbsr_amd::kRowWaves) units += s.rows[g].step_count >= 0 ? 1 : 0;
+  if (units <= int64_t(vbsr_amd::kXcds) * 192) {
+    CHECK(same(s.rows, s.rows_wide));
+  } else if (reorders) {
+    CHECK(!same(s.rows, s.rows_wide));
+  }
   const vbsr_amd::HostSchedule again = vbsr_amd::build_schedule(m);
   if (!(same(s.rows, again.rows) && same(s.rows_wide, again.rows_wide) && same(s.split.items, again.split.items) &&
         s.steps.size() == again.steps.size())) {
@@ -281,10 +286,10 @@ void check_view(const vbsr_host_view& m, const char* name, double max_seconds) {
               static_cast<long long>(s.groups), s.steps.size(), seconds);
 }
 
-void check_host(const vbsr_amd::HostMatrix& host, const char* name) {
+void check_host(const vbsr_amd::HostMatrix& host, const char* name, bool reorders = false) {
   const vbsr_host_view m = host.view();
   vbsr_amd::validate(m);
-  check_view(m, name, 30.0);
+  check_view(m, name, 30.0, reorders);
 }
 
 // Block row i uses block columns (i + j) mod cols, j < degree, all blocks
@@ -389,7 +394,7 @@ int main() {
     std::snprintf(name, sizeof(name), "rows=%d degree=%d dist=%d locality=%d seed=%llu", options.block_rows,
                   options.degree, options.distribution, options.locality,
                   static_cast<unsigned long long>(options.seed));
-    check_host(vbsr_amd::generate(options), name);
+    check_host(vbsr_amd::generate(options), name, shape[0] == 4096 && shape[2] >= 8);
   }
   check_host(with_empty_row(), "hand-made, empty middle row");
   check_shared_columns(16384, 8, 8);

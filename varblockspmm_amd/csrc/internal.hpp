@@ -123,10 +123,11 @@ struct HostSchedule {
 // each workgroup on the XCD whose eighth of the block columns holds most of
 // its rows' block widths (so an XCD's B slices concentrate in one eighth of
 // B), with equal work per XCD.  Within an XCD, `rows` runs the heaviest
-// workgroups first; `rows_wide` chains the shared workgroups (among the
-// heavier three quarters) whose rows share block columns and runs the rest
-// -- packed workgroups and the lightest quarter -- after them, heaviest
-// first.  Deterministic.
+// workgroups first; `rows_wide` chains the workgroups of the heavier three
+// quarters whose rows share block columns and runs the lightest quarter
+// after them, heaviest first -- when the matrix has more than 192
+// workgroups per XCD; below that it is heaviest first like `rows`.
+// Deterministic.
 HostSchedule build_schedule(const vbsr_host_view& host);
 
 // ---- device format (device_matrix.cpp) ----------------------------------

@@ -22,14 +22,17 @@
 //    columns this gives contiguous bands of rows;
 //  * within a band, two launch orders are kept.  For RHS 8 and 16 heavier
 //    rows are dispatched first, so the light ones fill the tail of the launch.
-//    For RHS 32 and 64, where B is most of the traffic, the shared rows
-//    among the heavier three quarters of the band are chained so that each
-//    row follows the rows it shares block columns (or neighbouring block
-//    columns, which share B's 128-byte lines) with; packed light rows and the
-//    lightest quarter follow, heaviest first.
-//    Chaining cuts the XCD's B line misses; keeping a light tail bounds the
-//    imbalance it costs.  On RHS 8 and 16, where A dominates, the imbalance
-//    outweighs the saving.
+//    For RHS 32 and 64, where B is most of the traffic, the workgroups among
+//    the heavier three quarters of the band are chained so that each follows
+//    the workgroups it shares block columns (or neighbouring block columns,
+//    which share B's 128-byte lines) with; the lightest quarter follows,
+//    heaviest first.  Chaining cuts the XCD's B line misses; keeping a light
+//    tail bounds the imbalance it costs.  It pays only when an XCD runs its
+//    workgroups in more than about one and a half rounds of its workgroup
+//    slots (128 at RHS 32, 96 at RHS 64), so matrices of at most
+//    kChainMinUnits workgroups per XCD (few rows, or degree 1) keep the
+//    heaviest-first order at RHS 32 and 64 too.  On RHS 8 and 16, where A
+//    dominates, the imbalance always outweighs the saving.
 #include <algorithm>
 #include <array>
 #include <numeric>
@@ -173,23 +176,22 @@ HostSchedule build_schedule(const vbsr_host_view& m) {
   // 3 * kMaxUsers updates per block instead of growing with the square of
   // the units that share a column.
   constexpr size_t kMaxUsers = 64;
+  // Chaining needs more than kChainMinUnits workgroups per XCD on average.
+  // Heaviest first instead of chaining, measured at RHS 32 / 64: 512 block
+  // rows of degree 8 -6% / -8%, 1024 rows -6% / +3%, 4096 rows of degree 1
+  // (every workgroup packed) -5% at RHS 32; from 2048 rows of degree 4 on
+  // chaining is as fast or faster (degree 2 at 4096 rows: -3% to -6%).
+  constexpr size_t kChainMinUnits = 192;
+  const bool chain = n_units > size_t(kXcds) * kChainMinUnits;
   std::vector<std::vector<int32_t>> users(static_cast<size_t>(cols));
   std::vector<std::vector<size_t>> chained(kXcds);
   for (int xcd = 0; xcd < kXcds; ++xcd) {
-    // The chain takes the shared units (a row dealt to all four waves) among
-    // the band's heavier three quarters; packed light units and the lightest
-    // quarter follow it in band order, heaviest first.  (Chaining packed
-    // units measured 11-16% slower at RHS 32 on matrices of degree 1.)
+    // The chain takes the band's heavier three quarters; the lightest
+    // quarter follows it in band order, heaviest first.
     const auto& sorted = bands[size_t(xcd)];
     const size_t n = sorted.size();
-    std::vector<size_t> band, tail;
-    for (size_t q = 0; q < n; ++q) {
-      const auto& unit = units[sorted[q]];
-      const bool shared = unit.size() == 1 && steps_of(unit[0]) > kPackSteps;
-      (q < n - n / 4 && shared ? band : tail).push_back(sorted[q]);
-    }
-    const size_t head = band.size();  // units chained
-    band.insert(band.end(), tail.begin(), tail.end());
+    const size_t head = chain ? n - n / 4 : 0;  // units chained
+    std::vector<size_t> band(sorted.begin(), sorted.end());
     for (auto& u : users) u.clear();
     auto for_each_col = [&](size_t unit, auto&& f) {
       for (const int32_t i : units[unit])
