@@ -154,10 +154,12 @@ int64_t vbsr_matrix_scalar_cols(const vbsr_matrix* matrix);
  * arrays owned by the matrix; opaque to callers. */
 typedef struct vbsr_row_schedule {
   const void* steps;     /* device: one 16-byte record per k step */
-  const void* rows;      /* device: four 48-byte wave items per workgroup, launch order for rhs 8 and 16 */
-  int64_t groups;        /* workgroups of one launch */
-  int32_t step_limit;    /* index of the last step record */
-  const void* rows_wide; /* device: the same row items, launch order for rhs 32 and 64 */
+  const void* rows;       /* device: four 48-byte wave items per workgroup, launch order for rhs 8 and 16 */
+  int64_t groups;         /* workgroups of a launch from rows or rows_wide */
+  int32_t step_limit;     /* index of the last step record */
+  const void* rows_wide;  /* device: the same row items, launch order for rhs 32 */
+  const void* rows_rhs64; /* device: row items for rhs 64, which packs longer light rows */
+  int64_t groups_rhs64;   /* workgroups of a launch from rows_rhs64 */
 } vbsr_row_schedule;
 int vbsr_matrix_row_schedule(const vbsr_matrix* matrix, vbsr_row_schedule* out);
 

@@ -2,17 +2,19 @@
 // from the library's own sources without a GPU.  For each matrix:
 //   * the step records cover every block of every row exactly once, in
 //     row_ptr order, with the A and B offsets the kernel reads;
-//   * both launch orders hold every block row once, in workgroups of four
-//     wave items: one shared row (rows of more than kPackSteps steps) or up
-//     to four packed light rows, one per wave; padding waves have
-//     step_count < 0; each item describes its row, including the wave's
-//     first step record;
-//   * both orders place each row on the same XCD (workgroup index mod 8), and
-//     no XCD's work exceeds an eighth of the total by more than one row's;
-//   * `rows` runs each XCD's workgroups heaviest first; `rows_wide`, for a
-//     matrix of more than 192 workgroups per XCD, chains the heavier three
-//     quarters of each XCD's band and ends it with the lightest quarter,
-//     heaviest first, and is heaviest first throughout otherwise;
+//   * the three launch orders (RHS 8/16, RHS 32, RHS 64) hold every block
+//     row once, in workgroups of four wave items: one shared row (rows of
+//     more than kPackSteps steps) or up to four packed light rows, one per
+//     wave; padding waves have step_count < 0; each item describes its row,
+//     including the wave's first step record;
+//   * `rows` and `rows_wide` place each row on the same XCD (workgroup index
+//     mod 8), as `rows_rhs64` does for its own workgroups (it packs rows of
+//     up to kPackStepsRhs64 steps), and no XCD's work exceeds an eighth of
+//     the total by more than one row's;
+//   * `rows` runs each XCD's workgroups heaviest first; `rows_wide` and
+//     `rows_rhs64`, for more than 192 workgroups per XCD, chain the heavier three
+//     quarters of each XCD's band and end it with the lightest quarter,
+//     heaviest first, and are heaviest first throughout otherwise;
 //   * the split-row schedule: each row's parts cover its steps in order and
 //     take consecutive virtual rows, every part is in exactly one workgroup,
 //     and the automatic choice follows its rule;
@@ -55,17 +57,17 @@ int64_t row_work(const vbsr_amd::WaveItem& item) { return int64_t((item.h + 15) 
 // the same XCD in both orders; per-XCD work within an eighth plus one
 // workgroup; the order of each XCD's workgroups.
 void check_order(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s,
-                 const std::vector<vbsr_amd::WaveItem>& items, std::vector<int>& xcd_of_row, bool wide) {
-  using vbsr_amd::kPackSteps;
+                 const std::vector<vbsr_amd::WaveItem>& items, std::vector<int>& xcd_of_row, bool wide,
+                 int64_t groups, int32_t pack_steps) {
   using vbsr_amd::kRowWaves;
   using vbsr_amd::kXcds;
-  CHECK(int64_t(items.size()) == s.groups * kRowWaves);
-  CHECK(s.groups % kXcds == 0);
+  CHECK(int64_t(items.size()) == groups * kRowWaves);
+  CHECK(groups % kXcds == 0);
   std::vector<int> seen(size_t(m.block_rows), 0);
   std::vector<int64_t> load(kXcds, 0);
   std::vector<std::vector<int64_t>> band_work(kXcds);
   bool padding_started[kXcds] = {};
-  for (int64_t g = 0; g < s.groups; ++g) {
+  for (int64_t g = 0; g < groups; ++g) {
     const auto* wg = &items[size_t(g) * kRowWaves];
     const int xcd = int(g % kXcds);
     if (wg[0].step_count < 0) {
@@ -91,11 +93,11 @@ void check_order(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s,
       int32_t first;
       if (shared) {
         CHECK(item.group == kRowWaves && item.lead == w && item.row == wg[0].row);
-        CHECK(item.step_count > kPackSteps);
+        CHECK(item.step_count > pack_steps);
         first = item.step_first + vbsr_amd::kStepRun * w;
       } else {
         CHECK(item.group == 1 && item.lead == 0);
-        CHECK(item.step_count <= kPackSteps);
+        CHECK(item.step_count <= pack_steps);
         first = item.step_first;
       }
       const bool has = first < item.step_first + item.step_count;
@@ -265,8 +267,11 @@ void check_view(const vbsr_host_view& m, const char* name, double max_seconds, b
   check_steps(m, s);
   check_split(m, s);
   std::vector<int> xcd_of_row(size_t(m.block_rows), -1);
-  check_order(m, s, s.rows, xcd_of_row, false);
-  check_order(m, s, s.rows_wide, xcd_of_row, true);
+  check_order(m, s, s.rows, xcd_of_row, false, s.groups, vbsr_amd::kPackSteps);
+  check_order(m, s, s.rows_wide, xcd_of_row, true, s.groups, vbsr_amd::kPackSteps);
+  // The RHS 64 order packs more rows, so it places its own workgroups.
+  std::vector<int> xcd_of_row64(size_t(m.block_rows), -1);
+  check_order(m, s, s.rows_rhs64, xcd_of_row64, true, s.groups_rhs64, vbsr_amd::kPackStepsRhs64);
   // Up to 192 workgroups per XCD the wide order is the heaviest-first one;
   // above it, on a random matrix, the chain reorders them.
   int64_t units = 0;
@@ -277,7 +282,8 @@ void check_view(const vbsr_host_view& m, const char* name, double max_seconds, b
     CHECK(!same(s.rows, s.rows_wide));
   }
   const vbsr_amd::HostSchedule again = vbsr_amd::build_schedule(m);
-  if (!(same(s.rows, again.rows) && same(s.rows_wide, again.rows_wide) && same(s.split.items, again.split.items) &&
+  if (!(same(s.rows, again.rows) && same(s.rows_wide, again.rows_wide) && same(s.rows_rhs64, again.rows_rhs64) &&
+        same(s.split.items, again.split.items) &&
         s.steps.size() == again.steps.size())) {
     std::fprintf(stderr, "FAILED: schedule not deterministic\n");
     ++failures;

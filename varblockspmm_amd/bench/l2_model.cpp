@@ -160,7 +160,11 @@ int main(int argc, char** argv) {
   const HostMatrix m = vbsr_amd::generate(g);
   const vbsr_host_view view = m.view();
   const HostSchedule s = vbsr_amd::build_schedule(view);
-  const std::vector<WaveItem>& items = o.order == "wide" ? s.rows_wide : s.rows;
+  // The wide order is the one the library launches at RHS 32, and at RHS 64
+  // with its own packing.
+  const bool wide64 = o.order == "wide" && o.rhs == 64;
+  const std::vector<WaveItem>& items = wide64 ? s.rows_rhs64 : o.order == "wide" ? s.rows_wide : s.rows;
+  const int64_t groups = wide64 ? s.groups_rhs64 : s.groups;
   const int64_t K = view.col_scalar_off[view.col_scalar_off_len - 1];
   const int64_t M = view.row_scalar_off[view.row_scalar_off_len - 1];
   const int64_t b_base = 0, c_base = (K * o.rhs * 4 / kLine + 1024) * kLine;
@@ -171,7 +175,7 @@ int main(int argc, char** argv) {
     // Workgroup start times: a list scheduler over the XCD's slots.
     std::priority_queue<double, std::vector<double>, std::greater<double>> free_at;
     for (int i = 0; i < kCusPerXcd * o.occupancy; ++i) free_at.push(0.0);
-    for (int64_t gi = xcd; gi < s.groups; gi += kXcds) {
+    for (int64_t gi = xcd; gi < groups; gi += kXcds) {
       const WaveItem* wg = &items[size_t(gi) * kRowWaves];
       if (wg[0].step_count < 0) continue;  // padding workgroup
       const double start = free_at.top();

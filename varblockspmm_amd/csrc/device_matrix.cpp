@@ -59,6 +59,8 @@ DeviceMatrix::DeviceMatrix(const vbsr_host_view& host) {
     schedule_.rows = upload(schedule.rows.data(), int64_t(schedule.rows.size()), allocations_);
     schedule_.rows_wide = upload(schedule.rows_wide.data(), int64_t(schedule.rows_wide.size()), allocations_);
     schedule_.groups = schedule.groups;
+    schedule_.rows_rhs64 = upload(schedule.rows_rhs64.data(), int64_t(schedule.rows_rhs64.size()), allocations_);
+    schedule_.groups_rhs64 = schedule.groups_rhs64;
     schedule_.step_limit = int32_t(std::max<size_t>(schedule.steps.size(), 1) - 1);
     split_.items = upload(schedule.split.items.data(), int64_t(schedule.split.items.size()), allocations_);
     split_.rows = upload(schedule.split.rows.data(), int64_t(schedule.split.rows.size()), allocations_);

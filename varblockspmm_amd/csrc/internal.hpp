@@ -62,6 +62,9 @@ constexpr int64_t kHalfStep = int64_t(1) << 62;
 constexpr int kRowWaves = 4;
 constexpr int kStepRun = 2;
 constexpr int kPackSteps = 4;
+// At RHS 64, whose k steps cost about twice those of RHS 32, rows of up to
+// kPackStepsRhs64 steps are packed.
+constexpr int kPackStepsRhs64 = 8;
 
 // One wave's work: its share of block row `row`, whose steps are
 // steps[step_first .. step_first + step_count).  `group` waves share the row
@@ -109,21 +112,24 @@ struct HostSplitSchedule {
 struct HostSchedule {
   std::vector<StepRec> steps;       // row after row, blocks in row_ptr order
   std::vector<WaveItem> rows;       // kRowWaves per workgroup, launch order for RHS 8 and 16
-  std::vector<WaveItem> rows_wide;  // the same workgroups, launch order for RHS 32 and 64
-  int64_t groups{};                 // workgroups of one launch (multiple of kXcds)
+  std::vector<WaveItem> rows_wide;  // the same workgroups, launch order for RHS 32
+  int64_t groups{};                 // workgroups of a launch from rows or rows_wide (multiple of kXcds)
+  std::vector<WaveItem> rows_rhs64; // workgroups packed at kPackStepsRhs64, in the rows_wide order, for RHS 64
+  int64_t groups_rhs64{};
   HostSplitSchedule split;
   // Whether Plan's automatic choice takes the split-row path: the row-owned
   // launch would leave most CUs idle while its rows are long.
   bool split_preferred{};
 };
 
-// Step records plus two launch orders of the workgroups.  Rows of at most
-// kPackSteps steps are packed kRowWaves to a workgroup (rows of similar work
-// together); every other row has a workgroup of its own.  Both orders place
+// Step records plus three launch orders of the workgroups.  Rows of at most
+// kPackSteps steps (kPackStepsRhs64 for the RHS 64 order) are packed
+// kRowWaves to a workgroup (rows of similar work together); every other row
+// has a workgroup of its own.  Both orders place
 // each workgroup on the XCD whose eighth of the block columns holds most of
 // its rows' block widths (so an XCD's B slices concentrate in one eighth of
 // B), with equal work per XCD.  Within an XCD, `rows` runs the heaviest
-// workgroups first; `rows_wide` chains the workgroups of the heavier three
+// workgroups first; `rows_wide` and `rows_rhs64` chain the workgroups of the heavier three
 // quarters whose rows share block columns and runs the lightest quarter
 // after them, heaviest first -- when the matrix has more than 192
 // workgroups per XCD; below that it is heaviest first like `rows`.

@@ -4,8 +4,9 @@
 //
 // Work unit.  One workgroup (4 waves) owns one block row of height h and
 // writes its h x RHS slab of C, or owns up to four light rows, one per wave
-// (the schedule packs rows of at most kPackSteps k steps); nothing else
-// writes those slabs, so there are no atomics and no global workspace.  A
+// (the schedule packs rows of at most kPackSteps k steps, kPackStepsRhs64 at
+// RHS 64); nothing else writes those slabs, so there are no atomics and no
+// global workspace.  A
 // row's k steps (16 columns of one block, or the 8 that end a block whose
 // width is 8 mod 16; one precomputed record each) are dealt to the waves
 // that share it -- four, in runs of two, or a packed row's one wave; each
@@ -604,9 +605,14 @@ void launch_row_owned_math(const vbsr_device_view& a, const vbsr_row_schedule& s
     throw std::invalid_argument(
         "row-owned kernel needs (min(rhs, 16) - 1) * K * 4 + 128 <= 0xfffffff0 (its 32-bit B offsets)");
   const void* rows = rhs >= 32 && s.rows_wide != nullptr ? s.rows_wide : s.rows;
+  int64_t groups = s.groups;
+  if (rhs == 64 && s.rows_rhs64 != nullptr) {
+    rows = s.rows_rhs64;
+    groups = s.groups_rhs64;
+  }
   const Launch L{a, static_cast<const StepRec*>(s.steps), static_cast<const WaveItem*>(rows), s.step_limit, b, c,
                  a.scalar_rows};
-  launch_items<kValu>(L, s.groups, rhs, stream);
+  launch_items<kValu>(L, groups, rhs, stream);
 }
 
 }  // namespace

@@ -68,174 +68,185 @@ HostSchedule build_schedule(const vbsr_host_view& m) {
   std::vector<int64_t> row_work(static_cast<size_t>(rows));
   for (int32_t i = 0; i < rows; ++i) row_work[size_t(i)] = int64_t((m.row_size[i] + 15) / 16) * steps_of(i);
 
-  // Workgroups ("units"): every row of more than kPackSteps steps alone;
-  // the light rows, heaviest first, kRowWaves at a time.  A unit's cost is
-  // its rows' work plus a fixed per-workgroup overhead.
-  std::vector<std::vector<int32_t>> units;
-  std::vector<int32_t> light;
-  for (int32_t i = 0; i < rows; ++i) {
-    if (steps_of(i) > kPackSteps)
-      units.push_back({i});
-    else
-      light.push_back(i);
-  }
-  std::stable_sort(light.begin(), light.end(),
-                   [&](int32_t x, int32_t y) { return row_work[size_t(x)] > row_work[size_t(y)]; });
-  for (size_t q = 0; q < light.size(); q += kRowWaves)
-    units.emplace_back(light.begin() + std::ptrdiff_t(q),
-                       light.begin() + std::ptrdiff_t(std::min(light.size(), q + size_t(kRowWaves))));
-  const size_t n_units = units.size();
-  std::vector<int64_t> work(n_units, 8);
-  for (size_t u = 0; u < n_units; ++u)
-    for (const int32_t i : units[u]) work[u] += row_work[size_t(i)];
-
-  // Home eighth of each unit: the eighth of the block columns holding the
-  // largest share of its rows' block widths.
-  const int32_t cols = m.block_cols;
-  std::vector<std::array<int64_t, kXcds>> share(n_units);
-  for (size_t u = 0; u < n_units; ++u) {
-    share[u].fill(0);
-    for (const int32_t i : units[u])
-      for (int32_t blk = m.row_ptr[i]; blk < m.row_ptr[i + 1]; ++blk) {
-        const int32_t c = m.block_col[blk];
-        share[u][size_t(std::min<int64_t>(kXcds - 1, int64_t(c) * kXcds / cols))] += m.col_size[c];
-      }
-  }
-  auto top_share = [&](size_t u) { return *std::max_element(share[u].begin(), share[u].end()); };
-  std::vector<size_t> order(n_units);
-  std::iota(order.begin(), order.end(), size_t(0));
-  std::stable_sort(order.begin(), order.end(), [&](size_t x, size_t y) { return top_share(x) > top_share(y); });
-
-  const int64_t total = std::accumulate(work.begin(), work.end(), int64_t(0));
-  const int64_t cap = total / kXcds + 1;
-  std::array<int64_t, kXcds> load{};
-  std::vector<std::vector<size_t>> bands(kXcds);
-  for (const size_t u : order) {
-    std::array<int, kXcds> rank{};
-    std::iota(rank.begin(), rank.end(), 0);
-    std::stable_sort(rank.begin(), rank.end(), [&](int x, int y) { return share[u][size_t(x)] > share[u][size_t(y)]; });
-    int chosen = -1;
-    for (const int x : rank)
-      if (load[size_t(x)] + work[u] <= cap) {
-        chosen = x;
-        break;
-      }
-    if (chosen < 0) chosen = int(std::min_element(load.begin(), load.end()) - load.begin());
-    bands[size_t(chosen)].push_back(u);
-    load[size_t(chosen)] += work[u];
-  }
-
-  int64_t per_xcd = 0;
-  for (auto& band : bands) {
-    std::stable_sort(band.begin(), band.end(), [&](size_t x, size_t y) { return work[x] > work[y]; });
-    per_xcd = std::max<int64_t>(per_xcd, int64_t(band.size()));
-  }
-  out.groups = per_xcd * kXcds;
-
-  // Lays the bands out in launch order: the unit at position pos of XCD x's
-  // band is workgroup pos * 8 + x; missing positions are padding
-  // workgroups, all of whose waves are idle.
-  auto emit = [&](const std::vector<std::vector<size_t>>& ordered, std::vector<WaveItem>& items) {
-    WaveItem idle{};
-    idle.step_count = -1;
-    idle.row = -1;
-    idle.group = 1;
-    items.assign(size_t(out.groups) * kRowWaves, idle);
-    for (int xcd = 0; xcd < kXcds; ++xcd) {
-      const auto& band = ordered[size_t(xcd)];
-      for (size_t pos = 0; pos < band.size(); ++pos) {
-        const auto& unit = units[band[pos]];
-        WaveItem* wg = &items[(pos * kXcds + size_t(xcd)) * kRowWaves];
-        const bool shared = steps_of(unit[0]) > kPackSteps;
-        for (int w = 0; w < kRowWaves; ++w) {
-          if (!shared && size_t(w) >= unit.size()) continue;
-          const int32_t i = shared ? unit[0] : unit[size_t(w)];
-          WaveItem& item = wg[w];
-          item.c_off = m.row_scalar_off[i];
-          item.step_first = step_first[size_t(i)];
-          item.step_count = steps_of(i);
-          item.h = m.row_size[i];
-          item.row = i;
-          item.group = shared ? kRowWaves : 1;
-          item.lead = shared ? w : 0;
-          const int32_t first = shared ? kStepRun * w : 0;
-          if (first < item.step_count) item.first = out.steps[size_t(item.step_first + first)];
-        }
-      }
+  // The workgroups of one launch, for rows of at most pack_steps steps
+  // packed kRowWaves to a workgroup, in the heaviest-first order (if asked
+  // for) and in the wide order; returns the launch's workgroup count.
+  auto launch_orders = [&](int32_t pack_steps, std::vector<WaveItem>* heaviest, std::vector<WaveItem>* chained_items,
+                           size_t* units_out) -> int64_t {
+    // Workgroups ("units"): every row of more than pack_steps steps alone;
+    // the light rows, heaviest first, kRowWaves at a time.  A unit's cost is
+    // its rows' work plus a fixed per-workgroup overhead.
+    std::vector<std::vector<int32_t>> units;
+    std::vector<int32_t> light;
+    for (int32_t i = 0; i < rows; ++i) {
+      if (steps_of(i) > pack_steps)
+        units.push_back({i});
+      else
+        light.push_back(i);
     }
-  };
-  emit(bands, out.rows);
+    std::stable_sort(light.begin(), light.end(),
+                     [&](int32_t x, int32_t y) { return row_work[size_t(x)] > row_work[size_t(y)]; });
+    for (size_t q = 0; q < light.size(); q += kRowWaves)
+      units.emplace_back(light.begin() + std::ptrdiff_t(q),
+                         light.begin() + std::ptrdiff_t(std::min(light.size(), q + size_t(kRowWaves))));
+    const size_t n_units = units.size();
+    std::vector<int64_t> work(n_units, 8);
+    for (size_t u = 0; u < n_units; ++u)
+      for (const int32_t i : units[u]) work[u] += row_work[size_t(i)];
 
-  // Chained order of each band for RHS 32 and 64.  A unit's affinity to the
-  // units already placed counts 2 per shared block column and 1 per
-  // neighbouring one; the next unit is the unplaced one of highest affinity,
-  // ties to the heavier (then earlier) unit.  Affinities only grow, so a
-  // max-heap with stale entries skipped finds it.  A block column used by
-  // more than kMaxUsers units of the band adds no affinity: it says little
-  // about which units belong together, and skipping it bounds the work by
-  // 3 * kMaxUsers updates per block instead of growing with the square of
-  // the units that share a column.
-  constexpr size_t kMaxUsers = 64;
-  // Chaining needs more than kChainMinUnits workgroups per XCD on average.
-  // Heaviest first instead of chaining, measured at RHS 32 / 64: 512 block
-  // rows of degree 8 -6% / -8%, 1024 rows -6% / +3%, 4096 rows of degree 1
-  // (every workgroup packed) -5% at RHS 32; from 2048 rows of degree 4 on
-  // chaining is as fast or faster (degree 2 at 4096 rows: -3% to -6%).
-  constexpr size_t kChainMinUnits = 192;
-  const bool chain = n_units > size_t(kXcds) * kChainMinUnits;
-  std::vector<std::vector<int32_t>> users(static_cast<size_t>(cols));
-  std::vector<std::vector<size_t>> chained(kXcds);
-  for (int xcd = 0; xcd < kXcds; ++xcd) {
-    // The chain takes the band's heavier three quarters; the lightest
-    // quarter follows it in band order, heaviest first.
-    const auto& sorted = bands[size_t(xcd)];
-    const size_t n = sorted.size();
-    const size_t head = chain ? n - n / 4 : 0;  // units chained
-    std::vector<size_t> band(sorted.begin(), sorted.end());
-    for (auto& u : users) u.clear();
-    auto for_each_col = [&](size_t unit, auto&& f) {
-      for (const int32_t i : units[unit])
-        for (int32_t blk = m.row_ptr[i]; blk < m.row_ptr[i + 1]; ++blk) f(m.block_col[blk]);
-    };
-    for (size_t q = 0; q < head; ++q) for_each_col(band[q], [&](int32_t c) { users[size_t(c)].push_back(int32_t(q)); });
-    // Heap keys: affinity in the high word, then the lower position (the
-    // band is sorted heaviest first, so that is the heavier unit).
-    auto key = [](uint64_t affinity, size_t q) { return (affinity << 32) | (0xffffffffu - uint32_t(q)); };
-    std::vector<uint32_t> affinity(head, 0), gain(head, 0);
-    std::vector<char> placed(head, 0);
-    std::vector<int32_t> touched;
-    std::priority_queue<uint64_t> heap;
-    for (size_t q = 0; q < head; ++q) heap.push(key(0, q));
-    auto& order_out = chained[size_t(xcd)];
-    while (!heap.empty()) {
-      const uint64_t top = heap.top();
-      heap.pop();
-      const size_t q = 0xffffffffu - uint32_t(top);
-      if (placed[q] || (top >> 32) != affinity[q]) continue;  // placed, or a stale entry
-      placed[q] = 1;
-      order_out.push_back(band[q]);
-      // Gains of the units this placement touches, summed first so that each
-      // touched unit is pushed once.
-      touched.clear();
-      for_each_col(band[q], [&](int32_t c) {
-        for (int32_t d = -1; d <= 1; ++d) {
-          if (c + d < 0 || c + d >= cols || users[size_t(c + d)].size() > kMaxUsers) continue;
-          for (const int32_t r : users[size_t(c + d)]) {
-            if (placed[size_t(r)]) continue;
-            if (gain[size_t(r)] == 0) touched.push_back(r);
-            gain[size_t(r)] += d == 0 ? 2 : 1;
+    // Home eighth of each unit: the eighth of the block columns holding the
+    // largest share of its rows' block widths.
+    const int32_t cols = m.block_cols;
+    std::vector<std::array<int64_t, kXcds>> share(n_units);
+    for (size_t u = 0; u < n_units; ++u) {
+      share[u].fill(0);
+      for (const int32_t i : units[u])
+        for (int32_t blk = m.row_ptr[i]; blk < m.row_ptr[i + 1]; ++blk) {
+          const int32_t c = m.block_col[blk];
+          share[u][size_t(std::min<int64_t>(kXcds - 1, int64_t(c) * kXcds / cols))] += m.col_size[c];
+        }
+    }
+    auto top_share = [&](size_t u) { return *std::max_element(share[u].begin(), share[u].end()); };
+    std::vector<size_t> order(n_units);
+    std::iota(order.begin(), order.end(), size_t(0));
+    std::stable_sort(order.begin(), order.end(), [&](size_t x, size_t y) { return top_share(x) > top_share(y); });
+
+    const int64_t total = std::accumulate(work.begin(), work.end(), int64_t(0));
+    const int64_t cap = total / kXcds + 1;
+    std::array<int64_t, kXcds> load{};
+    std::vector<std::vector<size_t>> bands(kXcds);
+    for (const size_t u : order) {
+      std::array<int, kXcds> rank{};
+      std::iota(rank.begin(), rank.end(), 0);
+      std::stable_sort(rank.begin(), rank.end(), [&](int x, int y) { return share[u][size_t(x)] > share[u][size_t(y)]; });
+      int chosen = -1;
+      for (const int x : rank)
+        if (load[size_t(x)] + work[u] <= cap) {
+          chosen = x;
+          break;
+        }
+      if (chosen < 0) chosen = int(std::min_element(load.begin(), load.end()) - load.begin());
+      bands[size_t(chosen)].push_back(u);
+      load[size_t(chosen)] += work[u];
+    }
+
+    int64_t per_xcd = 0;
+    for (auto& band : bands) {
+      std::stable_sort(band.begin(), band.end(), [&](size_t x, size_t y) { return work[x] > work[y]; });
+      per_xcd = std::max<int64_t>(per_xcd, int64_t(band.size()));
+    }
+    const int64_t groups = per_xcd * kXcds;
+    if (units_out != nullptr) *units_out = n_units;
+
+    // Lays the bands out in launch order: the unit at position pos of XCD x's
+    // band is workgroup pos * 8 + x; missing positions are padding
+    // workgroups, all of whose waves are idle.
+    auto emit = [&](const std::vector<std::vector<size_t>>& ordered, std::vector<WaveItem>& items) {
+      WaveItem idle{};
+      idle.step_count = -1;
+      idle.row = -1;
+      idle.group = 1;
+      items.assign(size_t(groups) * kRowWaves, idle);
+      for (int xcd = 0; xcd < kXcds; ++xcd) {
+        const auto& band = ordered[size_t(xcd)];
+        for (size_t pos = 0; pos < band.size(); ++pos) {
+          const auto& unit = units[band[pos]];
+          WaveItem* wg = &items[(pos * kXcds + size_t(xcd)) * kRowWaves];
+          const bool shared = steps_of(unit[0]) > pack_steps;
+          for (int w = 0; w < kRowWaves; ++w) {
+            if (!shared && size_t(w) >= unit.size()) continue;
+            const int32_t i = shared ? unit[0] : unit[size_t(w)];
+            WaveItem& item = wg[w];
+            item.c_off = m.row_scalar_off[i];
+            item.step_first = step_first[size_t(i)];
+            item.step_count = steps_of(i);
+            item.h = m.row_size[i];
+            item.row = i;
+            item.group = shared ? kRowWaves : 1;
+            item.lead = shared ? w : 0;
+            const int32_t first = shared ? kStepRun * w : 0;
+            if (first < item.step_count) item.first = out.steps[size_t(item.step_first + first)];
           }
         }
-      });
-      for (const int32_t r : touched) {
-        affinity[size_t(r)] += gain[size_t(r)];
-        gain[size_t(r)] = 0;
-        heap.push(key(affinity[size_t(r)], size_t(r)));
       }
+    };
+    if (heaviest != nullptr) emit(bands, *heaviest);
+
+    // Chained order of each band for RHS 32 and 64.  A unit's affinity to the
+    // units already placed counts 2 per shared block column and 1 per
+    // neighbouring one; the next unit is the unplaced one of highest affinity,
+    // ties to the heavier (then earlier) unit.  Affinities only grow, so a
+    // max-heap with stale entries skipped finds it.  A block column used by
+    // more than kMaxUsers units of the band adds no affinity: it says little
+    // about which units belong together, and skipping it bounds the work by
+    // 3 * kMaxUsers updates per block instead of growing with the square of
+    // the units that share a column.
+    constexpr size_t kMaxUsers = 64;
+    // Chaining needs more than kChainMinUnits workgroups per XCD on average.
+    // Heaviest first instead of chaining, measured at RHS 32 / 64: 512 block
+    // rows of degree 8 -6% / -8%, 1024 rows -6% / +3%, 4096 rows of degree 1
+    // (every workgroup packed) -5% at RHS 32; from 2048 rows of degree 4 on
+    // chaining is as fast or faster (degree 2 at 4096 rows: -3% to -6%).
+    constexpr size_t kChainMinUnits = 192;
+    const bool chain = n_units > size_t(kXcds) * kChainMinUnits;
+    std::vector<std::vector<int32_t>> users(static_cast<size_t>(cols));
+    std::vector<std::vector<size_t>> chained(kXcds);
+    for (int xcd = 0; xcd < kXcds; ++xcd) {
+      // The chain takes the band's heavier three quarters; the lightest
+      // quarter follows it in band order, heaviest first.
+      const auto& sorted = bands[size_t(xcd)];
+      const size_t n = sorted.size();
+      const size_t head = chain ? n - n / 4 : 0;  // units chained
+      std::vector<size_t> band(sorted.begin(), sorted.end());
+      for (auto& u : users) u.clear();
+      auto for_each_col = [&](size_t unit, auto&& f) {
+        for (const int32_t i : units[unit])
+          for (int32_t blk = m.row_ptr[i]; blk < m.row_ptr[i + 1]; ++blk) f(m.block_col[blk]);
+      };
+      for (size_t q = 0; q < head; ++q) for_each_col(band[q], [&](int32_t c) { users[size_t(c)].push_back(int32_t(q)); });
+      // Heap keys: affinity in the high word, then the lower position (the
+      // band is sorted heaviest first, so that is the heavier unit).
+      auto key = [](uint64_t affinity, size_t q) { return (affinity << 32) | (0xffffffffu - uint32_t(q)); };
+      std::vector<uint32_t> affinity(head, 0), gain(head, 0);
+      std::vector<char> placed(head, 0);
+      std::vector<int32_t> touched;
+      std::priority_queue<uint64_t> heap;
+      for (size_t q = 0; q < head; ++q) heap.push(key(0, q));
+      auto& order_out = chained[size_t(xcd)];
+      while (!heap.empty()) {
+        const uint64_t top = heap.top();
+        heap.pop();
+        const size_t q = 0xffffffffu - uint32_t(top);
+        if (placed[q] || (top >> 32) != affinity[q]) continue;  // placed, or a stale entry
+        placed[q] = 1;
+        order_out.push_back(band[q]);
+        // Gains of the units this placement touches, summed first so that each
+        // touched unit is pushed once.
+        touched.clear();
+        for_each_col(band[q], [&](int32_t c) {
+          for (int32_t d = -1; d <= 1; ++d) {
+            if (c + d < 0 || c + d >= cols || users[size_t(c + d)].size() > kMaxUsers) continue;
+            for (const int32_t r : users[size_t(c + d)]) {
+              if (placed[size_t(r)]) continue;
+              if (gain[size_t(r)] == 0) touched.push_back(r);
+              gain[size_t(r)] += d == 0 ? 2 : 1;
+            }
+          }
+        });
+        for (const int32_t r : touched) {
+          affinity[size_t(r)] += gain[size_t(r)];
+          gain[size_t(r)] = 0;
+          heap.push(key(affinity[size_t(r)], size_t(r)));
+        }
+      }
+      order_out.insert(order_out.end(), band.begin() + std::ptrdiff_t(head), band.end());
     }
-    order_out.insert(order_out.end(), band.begin() + std::ptrdiff_t(head), band.end());
-  }
-  emit(chained, out.rows_wide);
+    emit(chained, *chained_items);
+    return groups;
+  };
+  size_t n_units = 0;
+  out.groups = launch_orders(kPackSteps, &out.rows, &out.rows_wide, &n_units);
+  out.groups_rhs64 = launch_orders(kPackStepsRhs64, nullptr, &out.rows_rhs64, nullptr);
 
   // Split-row schedule.  Parts of a row hold part_steps consecutive steps (a
   // multiple of one run per wave, sized so that the parts of the whole
