@@ -9,8 +9,9 @@
 //    the kernel never walks block metadata: a wave loads the records of all
 //    its steps of a row with one load;
 //  * one workgroup owns one block row, or up to four light rows (at most
-//    kPackSteps k steps each), one per wave, so that rows too short to keep
-//    four waves busy do not leave three of them idle;
+//    kPackSteps k steps each; kPackStepsRhs64 in the RHS 64 order, whose
+//    steps cost twice as much), one per wave, so that rows too short to
+//    keep four waves busy do not leave three of them idle;
 //  * workgroups are dispatched to the 8 XCDs round-robin by index, so each
 //    XCD's rows (its band) are placed at indices x, x + 8, x + 16, ...;
 //  * a block row goes to the XCD whose eighth of the block columns holds the
