@@ -33,6 +33,14 @@
 //             offsets, four lanes per column and 16 columns per load, so
 //             each load reads sixteen 64-byte segments that straddle
 //             128-byte lines as B's do.
+//   write     1 GiB of zeros written once with plain 16-byte stores, after
+//             the flush.
+//   mixed_write, mixed_write_half_lines, mixed_write_shared_lines
+//             the mixed case plus 18.9 MB of stores (C's bytes at
+//             configuration 3, RHS 32): into whole lines, into the first
+//             halves of twice as many lines, or into lines whose halves two
+//             workgroups on different XCDs write (as adjacent block rows
+//             share the boundary lines of C's columns).
 //
 // Workgroup i runs on XCD i mod 8; the grid is a multiple of 8 and each
 // workgroup reads 16 KiB chunks i, i + grid, ..., so each XCD reads one
@@ -117,14 +125,34 @@ __global__ __launch_bounds__(kThreads) void region_kernel(const f32x4* __restric
 
 // The mixed case: lane loads alternate between `cold` (non-temporal, read
 // once) and `warm` (plain; index i mod warm_count, so it is swept
-// cold_count / warm_count times), kUnroll of each in flight.
+// cold_count / warm_count times), kUnroll of each in flight.  kWrite: on
+// every odd iteration each lane also stores its running sum, 16 bytes, to
+// `out`, which the workgroup's lanes fill with contiguous 4 KiB pieces
+// (write bytes about 5% of the read bytes, as C is of the row-owned
+// kernel's L2-miss reads at configuration 3).  kWrite 2 stores the same
+// vectors to the first 64 bytes of twice as many 128-byte lines, and kWrite
+// 3 shares those lines between workgroups 2p and 2p + 1 (on different XCDs):
+// one writes each line's first 64 bytes, the other its last 64, as
+// adjacent block rows share the boundary lines of C's columns.
+template <int kWrite>
 __global__ __launch_bounds__(kThreads) void mixed_kernel(const f32x4* __restrict__ cold, int64_t cold_count,
                                                          const f32x4* __restrict__ warm, int64_t warm_count,
-                                                         float* __restrict__ sink) {
+                                                         float* __restrict__ sink, f32x4* __restrict__ out) {
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
   const int64_t chunk = int64_t(kThreads) * kUnroll;
   const int64_t stride = int64_t(gridDim.x) * chunk;
-  for (int64_t base = int64_t(blockIdx.x) * chunk + threadIdx.x; base < cold_count; base += stride) {
+  int64_t iteration = 0;
+  for (int64_t base = int64_t(blockIdx.x) * chunk + threadIdx.x; base < cold_count; base += stride, ++iteration) {
+    if (kWrite != 0 && (iteration & 1)) {
+      const int64_t t = threadIdx.x, half_line = (t / 4) * 8 + t % 4;
+      if (kWrite == 1)
+        out[((iteration >> 1) * gridDim.x + blockIdx.x) * kThreads + t] = acc;
+      else if (kWrite == 2)
+        out[((iteration >> 1) * gridDim.x + blockIdx.x) * 2 * kThreads + half_line] = acc;
+      else
+        out[((iteration >> 1) * (gridDim.x / 2) + blockIdx.x / 2) * 2 * kThreads + half_line + 4 * (blockIdx.x % 2)] =
+            acc;
+    }
     f32x4 v[2 * kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -215,11 +243,26 @@ Result run(const float* buffer, int64_t bytes, int passes, const float* flush, i
   return {median, double(bytes) * passes / (median * 1e3)};
 }
 
+// Streaming writes of zeros, strided as read_kernel reads.
+__global__ __launch_bounds__(kThreads) void write_kernel(f32x4* __restrict__ data, int64_t count) {
+  const int64_t chunk = int64_t(kThreads) * kUnroll;
+  const int64_t stride = int64_t(gridDim.x) * chunk;
+  for (int64_t base = int64_t(blockIdx.x) * chunk + threadIdx.x; base < count; base += stride) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + int64_t(u) * kThreads;
+      if (i < count) data[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  }
+}
+
 // segments_k > 0: the warm reads are mixed_segments_kernel's B-shaped
 // segments of a segments_k x 32 panel at `warm`; the bytes counted are then
-// the cold bytes plus the same number of warm bytes requested.
+// the cold bytes plus the same number of warm bytes requested.  out != null:
+// mixed_kernel<true>, which also writes to `out` (see there).
 Result run_mixed(const float* cold, int64_t cold_bytes, const float* warm, int64_t warm_bytes, const float* flush,
-                 int64_t flush_bytes, int reps, int grid, float* sink, hipStream_t stream, int64_t segments_k = 0) {
+                 int64_t flush_bytes, int reps, int grid, float* sink, hipStream_t stream, int64_t segments_k = 0,
+                 float* out = nullptr, int write_mode = 1) {
   hipEvent_t start, stop;
   check(hipEventCreateWithFlags(&start, hipEventDisableSystemFence), "hipEventCreate");
   check(hipEventCreateWithFlags(&stop, hipEventDisableSystemFence), "hipEventCreate");
@@ -233,9 +276,22 @@ Result run_mixed(const float* cold, int64_t cold_bytes, const float* warm, int64
     if (segments_k > 0)
       mixed_segments_kernel<<<grid, kThreads, 0, stream>>>(reinterpret_cast<const f32x4*>(cold), cold_bytes / 16, warm,
                                                            segments_k, sink);
+    else if (out != nullptr && write_mode == 1)
+      mixed_kernel<1><<<grid, kThreads, 0, stream>>>(reinterpret_cast<const f32x4*>(cold), cold_bytes / 16,
+                                                     reinterpret_cast<const f32x4*>(warm), warm_bytes / 16, sink,
+                                                     reinterpret_cast<f32x4*>(out));
+    else if (out != nullptr && write_mode == 2)
+      mixed_kernel<2><<<grid, kThreads, 0, stream>>>(reinterpret_cast<const f32x4*>(cold), cold_bytes / 16,
+                                                     reinterpret_cast<const f32x4*>(warm), warm_bytes / 16, sink,
+                                                     reinterpret_cast<f32x4*>(out));
+    else if (out != nullptr)
+      mixed_kernel<3><<<grid, kThreads, 0, stream>>>(reinterpret_cast<const f32x4*>(cold), cold_bytes / 16,
+                                                     reinterpret_cast<const f32x4*>(warm), warm_bytes / 16, sink,
+                                                     reinterpret_cast<f32x4*>(out));
     else
-      mixed_kernel<<<grid, kThreads, 0, stream>>>(reinterpret_cast<const f32x4*>(cold), cold_bytes / 16,
-                                                  reinterpret_cast<const f32x4*>(warm), warm_bytes / 16, sink);
+      mixed_kernel<0><<<grid, kThreads, 0, stream>>>(reinterpret_cast<const f32x4*>(cold), cold_bytes / 16,
+                                                     reinterpret_cast<const f32x4*>(warm), warm_bytes / 16, sink,
+                                                     nullptr);
     check(hipEventRecord(stop, stream), "record");
     check(hipEventSynchronize(stop), "sync");
     float ms = 0;
@@ -298,6 +354,32 @@ int main(int argc, char** argv) {
     }
   }
   {
+    // Write ceiling: 1 GiB of zeros into `dram` (which holds zeros).
+    hipEvent_t start, stop;
+    check(hipEventCreate(&start), "hipEventCreate");
+    check(hipEventCreate(&stop), "hipEventCreate");
+    std::vector<double> us;
+    for (int r = 0; r < reps + 1; ++r) {
+      read_kernel<false><<<grid, kThreads, 0, stream>>>(reinterpret_cast<const f32x4*>(flush), GiB / 16, 1, sink);
+      check(hipEventRecord(start, stream), "record");
+      write_kernel<<<grid, kThreads, 0, stream>>>(reinterpret_cast<f32x4*>(dram), GiB / 16);
+      check(hipEventRecord(stop, stream), "record");
+      check(hipEventSynchronize(stop), "sync");
+      float ms = 0;
+      check(hipEventElapsedTime(&ms, start, stop), "elapsed");
+      if (r > 0) us.push_back(double(ms) * 1000.0);
+    }
+    check(hipGetLastError(), "launch");
+    std::sort(us.begin(), us.end());
+    const double median = us[us.size() / 2];
+    std::printf("{\"case\": \"write\", \"stores\": \"plain\", \"bytes_per_pass\": %lld, \"passes\": 1, "
+                "\"median_us\": %.2f, \"GB_per_s\": %.1f, \"grid\": %d, \"reps\": %d}\n",
+                static_cast<long long>(GiB), median, double(GiB) / (median * 1e3), grid, reps);
+    std::fflush(stdout);
+    check(hipEventDestroy(start), "destroy");
+    check(hipEventDestroy(stop), "destroy");
+  }
+  {
     // The mixed case reads the first 168 MiB of `dram` cold and the last
     // 84 MiB of `flush` warm (the rest of `flush` is the flush); it counts
     // 2 x 168 MiB per launch.
@@ -308,6 +390,30 @@ int main(int argc, char** argv) {
                 "\"passes\": 1, \"median_us\": %.2f, \"GB_per_s\": %.1f, \"grid\": %d, \"reps\": %d}\n",
                 static_cast<long long>(2 * cold_bytes), r.median_us, r.gbps, grid, reps);
     std::fflush(stdout);
+    // The same with stores on every odd iteration: a lane iterates at most
+    // ceil(cold / stride) times, and its odd iterations write rows
+    // 0 .. iterations / 2 of a grid x kThreads array of 16-byte vectors.
+    const int64_t stride = int64_t(grid) * kThreads * kUnroll;
+    const int64_t iterations = (cold_bytes / 16 + stride - 1) / stride;
+    const int64_t out_vectors = (iterations / 2 + 1) * grid * 2 * kThreads;  // room for write modes 1-3
+    int64_t written = 0;  // vectors stored: lanes whose odd iteration j runs
+    for (int64_t j = 1; j < iterations; j += 2)
+      for (int64_t b = 0; b < grid; ++b)
+        written += std::clamp<int64_t>(cold_bytes / 16 - j * stride - b * kThreads * kUnroll, 0, kThreads);
+    float* out = nullptr;
+    check(hipMalloc(&out, size_t(out_vectors) * 16), "hipMalloc");
+    const char* write_names[] = {"", "mixed_write", "mixed_write_half_lines", "mixed_write_shared_lines"};
+    for (int mode = 1; mode <= 3; ++mode) {
+      const Result w = run_mixed(dram, cold_bytes, flush + (GiB - warm_bytes) / 4, warm_bytes, flush,
+                                 GiB - warm_bytes, reps, grid, sink, stream, 0, out, mode);
+      std::printf("{\"case\": \"%s\", \"loads\": \"nontemporal cold + plain warm + plain stores\", "
+                  "\"bytes_per_pass\": %lld, \"bytes_written\": %lld, \"passes\": 1, \"median_us\": %.2f, "
+                  "\"GB_per_s\": %.1f, \"grid\": %d, \"reps\": %d}\n",
+                  write_names[mode], static_cast<long long>(2 * cold_bytes), static_cast<long long>(written * 16),
+                  w.median_us, w.gbps, grid, reps);
+      std::fflush(stdout);
+    }
+    check(hipFree(out), "hipFree");
     // B-shaped warm reads: a 145,304 x 32 panel (18.6 MB) at the end of `flush`.
     const int64_t k_rows = 145304, panel_bytes = k_rows * 32 * 4;
     const Result s = run_mixed(dram, cold_bytes, flush + (GiB - panel_bytes) / 4, panel_bytes, flush,
