@@ -187,18 +187,28 @@ int vbsr_plan_launch_count(const vbsr_plan* plan);
 /* launch_row_owned (vbsr.hpp:158-159; row_owned.cu:397-423): the tuned
  * row-owned kernel for `rhs` over `matrix`, scheduled by `schedule` (from
  * vbsr_matrix_row_schedule of the matrix that `matrix` views; the reference
- * passes row_shape_order/small/large in the same role).  K must be at most
- * 153,391,684 at rhs 8 and 71,582,785 otherwise, so that B offsets within a
- * 16-column tile fit 32 bits (VBSR_INVALID_ARGUMENT otherwise;
- * vbsr_plan_execute takes any K). */
+ * passes row_shape_order/small/large in the same role).  Any K: B is read
+ * through 32-bit offsets within a 16-column tile up to K = 153,391,684 at
+ * rhs 8 and 71,582,785 otherwise, and through 64-bit lane addresses past
+ * that. */
 int vbsr_launch_row_owned(const vbsr_device_view* matrix, const vbsr_row_schedule* schedule,
                           const float* B, float* C, int32_t rhs, hipStream_t stream);
+
+/* vbsr_launch_row_owned with B read through 64-bit lane addresses at every
+ * K: the form vbsr_launch_row_owned and vbsr_plan_execute take past the
+ * 32-bit offset bound, here at any K, so that it can be checked against the
+ * offset form (the results are bit-identical: only the addressing differs).
+ * No counterpart in the reference. */
+int vbsr_launch_row_owned_wide_b(const vbsr_device_view* matrix, const vbsr_row_schedule* schedule,
+                                 const float* B, float* C, int32_t rhs, hipStream_t stream);
 
 /* vbsr_launch_row_owned with plain FP32 multiply-adds (one fmaf per output
  * and k, k ascending within each step) in place of the MFMA tiles: the same
  * schedule, loads and LDS staging, within the same tolerance.  No
  * counterpart in the reference; kept as the measured alternative to the
- * MFMA kernel, which is faster at every RHS width (bench.py --kernel valu). */
+ * MFMA kernel, which is faster at every RHS width (bench.py --kernel valu).
+ * Unlike the MFMA kernel, it keeps the 32-bit B offset bound on K
+ * (VBSR_INVALID_ARGUMENT past it). */
 int vbsr_launch_row_owned_valu(const vbsr_device_view* matrix, const vbsr_row_schedule* schedule,
                                const float* B, float* C, int32_t rhs, hipStream_t stream);
 
@@ -211,7 +221,7 @@ int vbsr_launch_row_owned_valu(const vbsr_device_view* matrix, const vbsr_row_sc
  * row-owned kernel's tolerance of cpu_reference.  `workspace` is a device
  * buffer of at least vbsr_split_row_workspace_bytes(matrix, rhs) bytes,
  * 4-byte aligned, overlapping neither B nor C, that no other launch uses
- * until this one has finished.  K is bounded as for vbsr_launch_row_owned.
+ * until this one has finished.  Any K, as for vbsr_launch_row_owned.
  * Two launches; allocates nothing. */
 int vbsr_split_row_workspace_bytes(const vbsr_matrix* matrix, int32_t rhs, int64_t* bytes);
 int vbsr_launch_split_row(const vbsr_matrix* matrix, const float* B, float* C, int32_t rhs, void* workspace,

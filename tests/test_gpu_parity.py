@@ -357,6 +357,39 @@ def test_edge_matrices(name, rhs):
     c.close()
 
 
+WIDE_B_MATRICES = {**EDGE_MATRICES,
+                   "generated-high": lambda: vb.generate(48, 48, 8, "high", "random", 3),
+                   "generated-bimodal": lambda: vb.generate(40, 40, 4, "bimodal", "local", 5)}
+
+
+@pytest.mark.parametrize("rhs", [8, 16, 32, 64])
+@pytest.mark.parametrize("name", list(WIDE_B_MATRICES))
+def test_wide_b_addressing_is_bit_identical(name, rhs):
+    """B read through 64-bit lane addresses (the form launch_row_owned and the plan take past the
+    32-bit offset bound), forced at small K: bit-identical to the offset form, with finite B and with
+    +Inf in the first eight entries of every second block column, which the upper half of the
+    preceding column's half step would read (so a lane that loads where the offset form gets zeros
+    turns 0 * Inf into NaN)."""
+    note(f"wide B {name} rhs={rhs}")
+    host = WIDE_B_MATRICES[name]()
+    c = Case(host, rhs, 23)
+    view, schedule = c.matrix.device_view(), c.matrix.row_schedule()
+    for label in ("finite", "inf"):
+        if label == "inf":
+            b = c.b.reshape(rhs, host.scalar_cols).copy()
+            for col in range(1, host.block_cols, 2):
+                start = int(host.col_scalar_off[col])
+                b[:, start:start + 8] = np.inf
+            c.b = b.reshape(-1).copy()
+            c.b_dev = torch.from_numpy(c.b).to(DEVICE)
+        narrow = c.run(lambda: vb.launch_row_owned(view, schedule, c.b_dev, c.c_dev, rhs, c.stream))
+        wide = c.run(lambda: vb.launch_row_owned_wide_b(view, schedule, c.b_dev, c.c_dev, rhs, c.stream))
+        assert narrow.tobytes() == wide.tobytes(), f"{name} rhs={rhs} {label}: wide B differs"
+        if label == "finite":
+            c.check_tolerance(wide, f"{name} wide B")
+    c.close()
+
+
 @pytest.mark.parametrize("rhs", [8, 16, 32, 64])
 def test_unused_b_entries_never_reach_c(rhs):
     """NaN in every B row that no block references (including the rows right
@@ -720,28 +753,40 @@ def test_largest_b_offsets_take_the_mfma_kernel(scalar_cols, rhs):
         matrix.close()
 
 
-def test_k_at_the_offset_limit_goes_to_the_order_preserving_kernel():
-    """One block column past the largest K at RHS 16: the MFMA launcher refuses it and the plan runs
-    the order-preserving kernel."""
-    scalar_cols, rhs = 71_582_848, 16
-    note(f"offset limit: K={scalar_cols} rhs={rhs}")
+@pytest.mark.parametrize("scalar_cols,rhs", [(71_582_848, 16), (153_391_744, 8)])
+def test_k_past_the_offset_limit_stays_on_the_mfma_kernel(scalar_cols, rhs):
+    """One block column past the largest K the 32-bit B offsets reach: launch_row_owned and the plan
+    address B with 64-bit lane pointers instead, match the oracle, agree bit for bit with
+    launch_row_owned_wide_b and with each other, and repeat bit for bit; the VALU variant, which keeps
+    the offset bound, refuses the matrix."""
+    note(f"past the offset limit: K={scalar_cols} rhs={rhs} (B {scalar_cols * rhs * 4 / 2**30:.1f} GiB)")
     host, b = largest_offset_case(scalar_cols, rhs)
     matrix = vb.Matrix(host)
     try:
         stream = torch.cuda.Stream(device=DEVICE)
         b_dev = torch.from_numpy(b).to(DEVICE)
         c_dev = torch.full((host.scalar_rows * rhs,), float("nan"), device=DEVICE)
-        torch.cuda.synchronize()
-        with pytest.raises(ValueError):
-            vb.launch_row_owned(matrix.device_view(), matrix.row_schedule(), b_dev, c_dev, rhs, stream)
+        view, schedule = matrix.device_view(), matrix.row_schedule()
+
+        def run(launch):
+            c_dev.fill_(float("nan"))
+            torch.cuda.synchronize()
+            with torch.cuda.stream(stream):
+                launch()
+            stream.synchronize()
+            return c_dev.cpu().numpy().copy()
+
+        first = run(lambda: vb.launch_row_owned(view, schedule, b_dev, c_dev, rhs, stream))
+        check_against_oracle(host, b, rhs, first, "launch_row_owned past the limit")
+        assert run(lambda: vb.launch_row_owned(view, schedule, b_dev, c_dev, rhs, stream)).tobytes() == first.tobytes()
+        wide = run(lambda: vb.launch_row_owned_wide_b(view, schedule, b_dev, c_dev, rhs, stream))
+        assert wide.tobytes() == first.tobytes(), "launch_row_owned_wide_b differs"
         plan = vb.Plan(matrix, rhs)
-        with torch.cuda.stream(stream):
-            plan.execute(b_dev, c_dev, stream)
-        stream.synchronize()
-        result = c_dev.cpu().numpy()
-        check_against_oracle(host, b, rhs, result, "plan at the limit")
-        expected = o.fmaf_order(as_oracle(host), b, rhs)
-        assert result.tobytes() == expected.tobytes(), "plan did not take the order-preserving kernel"
+        assert plan.launch_count() == 1
+        planned = run(lambda: plan.execute(b_dev, c_dev, stream))
+        assert planned.tobytes() == first.tobytes(), "plan differs from launch_row_owned"
+        with pytest.raises(ValueError):
+            vb.launch_row_owned_valu(view, schedule, b_dev, c_dev, rhs, stream)
         plan.close()
         del b_dev, c_dev
     finally:

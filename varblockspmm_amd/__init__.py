@@ -86,6 +86,8 @@ SIGNATURES = {
     "vbsr_plan_launch_count": (ctypes.c_int, [_P]),
     "vbsr_launch_row_owned": (ctypes.c_int, [ctypes.POINTER(DeviceView), ctypes.POINTER(RowSchedule), _P, _P,
                                              ctypes.c_int32, _P]),
+    "vbsr_launch_row_owned_wide_b": (ctypes.c_int, [ctypes.POINTER(DeviceView), ctypes.POINTER(RowSchedule), _P, _P,
+                                                    ctypes.c_int32, _P]),
     "vbsr_launch_row_owned_scalar": (ctypes.c_int, [ctypes.POINTER(DeviceView), _P, _P, ctypes.c_int32, _P]),
     "vbsr_launch_row_owned_valu": (ctypes.c_int, [ctypes.POINTER(DeviceView), ctypes.POINTER(RowSchedule), _P, _P,
                                                   ctypes.c_int32, _P]),
@@ -331,6 +333,15 @@ def launch_row_owned(device_view, schedule, B, C, rhs, stream=None):
     _check_panel(C, device_view.scalar_rows * int(rhs), "C")
     _check(library().vbsr_launch_row_owned(ctypes.byref(device_view), ctypes.byref(schedule), _address(B),
                                            _address(C), int(rhs), _stream(stream)))
+
+
+def launch_row_owned_wide_b(device_view, schedule, B, C, rhs, stream=None):
+    """launch_row_owned with B read through 64-bit lane addresses at any K (the form it takes past
+    the 32-bit offset bound); bit-identical to launch_row_owned."""
+    _check_panel(B, device_view.scalar_cols * int(rhs), "B")
+    _check_panel(C, device_view.scalar_rows * int(rhs), "C")
+    _check(library().vbsr_launch_row_owned_wide_b(ctypes.byref(device_view), ctypes.byref(schedule), _address(B),
+                                                  _address(C), int(rhs), _stream(stream)))
 
 
 def launch_row_owned_valu(device_view, schedule, B, C, rhs, stream=None):

@@ -170,6 +170,15 @@ int vbsr_launch_row_owned(const vbsr_device_view* matrix, const vbsr_row_schedul
   });
 }
 
+int vbsr_launch_row_owned_wide_b(const vbsr_device_view* matrix, const vbsr_row_schedule* schedule,
+                                 const float* B, float* C, int32_t rhs, hipStream_t stream) {
+  return guarded([&] {
+    require(matrix, "matrix");
+    require(schedule, "schedule");
+    vbsr_amd::launch_row_owned_wide_b(*matrix, *schedule, B, C, rhs, stream);
+  });
+}
+
 int vbsr_split_row_workspace_bytes(const vbsr_matrix* matrix, int32_t rhs, int64_t* bytes) {
   return guarded([&] {
     require(matrix, "matrix");

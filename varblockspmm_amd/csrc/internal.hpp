@@ -197,24 +197,27 @@ inline void check_panels(const vbsr_device_view& a, const float* b, const float*
 void launch_scalar(const vbsr_device_view& a, const float* b, float* c, int rhs, hipStream_t stream);
 
 // Row-owned MFMA kernel (row_owned_mfma.hip).  Launch count: 1 (0 for an
-// empty schedule).  Requires row_owned_supported(a, b, c, rhs): float-aligned
-// B and C, and K small enough for 32-bit B offsets within a 16-column tile
-// (K <= 153,391,684 at rhs 8, 71,582,785 otherwise).
-// The same kernel with the MFMA tiles replaced by one fmaf per output and k
-// (same schedule, loads and LDS staging): the measured alternative to MFMA,
-// slower at every width.
-void launch_row_owned_valu(const vbsr_device_view& a, const vbsr_row_schedule& schedule, const float* b, float* c,
-                           int rhs, hipStream_t stream);
-bool row_owned_k_supported(const vbsr_device_view& a, int rhs);
-bool row_owned_supported(const vbsr_device_view& a, const float* b, const float* c, int rhs);
+// empty schedule); any K.  B is read through 32-bit buffer offsets within a
+// 16-column tile while narrow_b_offsets(a, rhs) holds (K <= 153,391,684 at
+// rhs 8, 71,582,785 otherwise), and through 64-bit lane addresses past that
+// (the same kernel otherwise; launch_row_owned_wide_b takes that form at any
+// K, with bit-identical results).
+bool narrow_b_offsets(const vbsr_device_view& a, int rhs);
 void launch_row_owned(const vbsr_device_view& a, const vbsr_row_schedule& schedule, const float* b, float* c,
                       int rhs, hipStream_t stream);
+void launch_row_owned_wide_b(const vbsr_device_view& a, const vbsr_row_schedule& schedule, const float* b, float* c,
+                             int rhs, hipStream_t stream);
+// The same kernel with the MFMA tiles replaced by one fmaf per output and k
+// (same schedule, loads and LDS staging): the measured alternative to MFMA,
+// slower at every width.  Needs narrow_b_offsets(a, rhs).
+void launch_row_owned_valu(const vbsr_device_view& a, const vbsr_row_schedule& schedule, const float* b, float* c,
+                           int rhs, hipStream_t stream);
 
 // The split-row path: the row-owned kernel over the matrix's split schedule
 // into `workspace` (split.virtual_rows * rhs floats), then the fixed-order
 // sum of each row's partial slabs into C.  Two launches; the workspace is
 // the caller's (a plan's own, or any buffer of at least that size that does
-// not overlap B or C).  Requires row_owned_supported(a, b, c, rhs).
+// not overlap B or C).  Any K, as for launch_row_owned.
 int64_t split_workspace_floats(const DeviceMatrix::Split& split, int rhs);
 void launch_split_row(const vbsr_device_view& a, const vbsr_row_schedule& schedule, const DeviceMatrix::Split& split,
                       const float* b, float* c, int rhs, float* workspace, int64_t workspace_floats,

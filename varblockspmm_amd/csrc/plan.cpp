@@ -16,10 +16,9 @@
 // row-owned launch would leave most CUs idle while their rows are long (few
 // block rows of high degree); Kernel::RowOwned never does.
 //
-// Matrices with more scalar columns than the MFMA kernel's 32-bit B offsets
-// reach (K > 153,391,684 at RHS 8, K > 71,582,785 otherwise) go to the
-// order-preserving kernel, which has no such limit.  Any float-aligned B and
-// C panels stay on the MFMA kernel.
+// Every K stays on the MFMA kernel: past the reach of its 32-bit B offsets
+// (K > 153,391,684 at RHS 8, K > 71,582,785 otherwise) it addresses B with
+// 64-bit lane pointers instead.
 #include <hip/hip_runtime_api.h>
 
 #include "internal.hpp"
@@ -45,9 +44,7 @@ Plan::~Plan() {
 }
 
 void Plan::execute(const float* b, float* c, hipStream_t stream) const {
-  if (!row_owned_supported(a_, b, c, options_.rhs_width))
-    launch_scalar(a_, b, c, options_.rhs_width, stream);
-  else if (split_row_)
+  if (split_row_)
     launch_split_row(a_, schedule_, split_, b, c, options_.rhs_width, workspace_, workspace_floats_, stream);
   else
     launch_row_owned(a_, schedule_, b, c, options_.rhs_width, stream);
@@ -55,9 +52,6 @@ void Plan::execute(const float* b, float* c, hipStream_t stream) const {
 
 int Plan::launch_count() const {
   if (a_.block_rows <= 0) return 0;
-  // The order-preserving kernel (K beyond the MFMA kernel's offsets) is one
-  // launch.
-  if (!row_owned_k_supported(a_, options_.rhs_width)) return 1;
   if (split_row_) return 2;
   return schedule_.groups > 0 ? 1 : 0;
 }
