@@ -53,9 +53,11 @@ def parse():
     p.add_argument("--locality", default="random")
     p.add_argument("--rhs", type=int, default=32)
     p.add_argument("--seed", type=int, default=1)
-    p.add_argument("--kernel", choices=["plan", "scalar", "valu"], default="plan",
+    p.add_argument("--kernel", choices=["plan", "scalar", "valu", "wide_b"], default="plan",
                    help="plan = the library's Plan::execute; scalar = the order-preserving kernel; valu = the "
-                        "row-owned kernel with plain FP32 multiply-adds instead of MFMA (the measured alternative)")
+                        "row-owned kernel with plain FP32 multiply-adds instead of MFMA (the measured alternative); "
+                        "wide_b = the row-owned kernel reading B through 64-bit addresses, the form it takes past "
+                        "the 32-bit offset bound on K")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-parity", action="store_true")
     p.add_argument("--calibrate-copy-mib", type=int, default=0,
@@ -222,6 +224,8 @@ def main():
             plan.execute(b_dev, c_dev, stream)
         elif args.kernel == "valu":
             vb.launch_row_owned_valu(view, schedule, b_dev, c_dev, args.rhs, stream)
+        elif args.kernel == "wide_b":
+            vb.launch_row_owned_wide_b(view, schedule, b_dev, c_dev, args.rhs, stream)
         else:
             vb.launch_row_owned_scalar(view, b_dev, c_dev, args.rhs, stream)
 
