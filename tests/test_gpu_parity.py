@@ -757,8 +757,9 @@ def test_largest_b_offsets_take_the_mfma_kernel(scalar_cols, rhs):
 def test_k_past_the_offset_limit_stays_on_the_mfma_kernel(scalar_cols, rhs):
     """One block column past the largest K the 32-bit B offsets reach: launch_row_owned and the plan
     address B with 64-bit lane pointers instead, match the oracle, agree bit for bit with
-    launch_row_owned_wide_b and with each other, and repeat bit for bit; the VALU variant, which keeps
-    the offset bound, refuses the matrix."""
+    launch_row_owned_wide_b and with each other, and repeat bit for bit; the split-row path (same
+    kernel, over row parts) matches the oracle too; the VALU variant, which keeps the offset bound,
+    refuses the matrix."""
     note(f"past the offset limit: K={scalar_cols} rhs={rhs} (B {scalar_cols * rhs * 4 / 2**30:.1f} GiB)")
     host, b = largest_offset_case(scalar_cols, rhs)
     matrix = vb.Matrix(host)
@@ -785,6 +786,8 @@ def test_k_past_the_offset_limit_stays_on_the_mfma_kernel(scalar_cols, rhs):
         assert plan.launch_count() == 1
         planned = run(lambda: plan.execute(b_dev, c_dev, stream))
         assert planned.tobytes() == first.tobytes(), "plan differs from launch_row_owned"
+        split = run(lambda: vb.launch_split_row_static(matrix, b_dev, c_dev, rhs, stream))
+        check_against_oracle(host, b, rhs, split, "split-row path past the limit")
         with pytest.raises(ValueError):
             vb.launch_row_owned_valu(view, schedule, b_dev, c_dev, rhs, stream)
         plan.close()
