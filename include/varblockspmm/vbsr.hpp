@@ -14,8 +14,9 @@
 //  - launch_row_owned takes the matrix's row schedule instead of the
 //    reference's row_shape_order and h <= 16 partition counts.
 //  - Kernel::SplitRow, reserved and rejected in the reference, selects the
-//    split-row path (also reachable as launch_split_row); Kernel::Auto takes
-//    it for few long rows.
+//    split-row path (also reachable as launch_split_row).  Kernel::Auto runs
+//    the row-owned kernel, as the reference's does; split_row_advised says
+//    when the split would pay.
 #pragma once
 
 #include <cstdint>
@@ -177,9 +178,12 @@ inline std::vector<float> cpu_reference(const HostMatrix& matrix, const std::vec
   return C;
 }
 
-/** Kernel selection (reference vbsr.hpp:91).  SplitRow, reserved in the
- * reference, is the split-row path here (two launches, a plan-owned
- * workspace); Auto takes it for few long rows, else RowOwned. */
+/** Kernel selection (reference vbsr.hpp:91).  Auto and RowOwned run the
+ * row-owned kernel (no workspace; a plan may execute on several streams at
+ * once), as in the reference.  SplitRow, reserved in the reference, is the
+ * split-row path here: two launches and a plan-owned workspace, so one such
+ * plan (or a copy of it, which shares the workspace) must not execute on two
+ * streams at once. */
 enum class Kernel { Auto, RowOwned, SplitRow };
 
 /** Configuration for a reusable execution plan (reference vbsr.hpp:94-97). */
@@ -274,6 +278,15 @@ inline int64_t split_row_workspace_bytes(const Matrix& matrix, int rhs) {
   int64_t bytes = 0;
   detail::check(vbsr_split_row_workspace_bytes(matrix.handle(), rhs, &bytes));
   return bytes;
+}
+
+/** Whether the split-row path is expected to beat the row-owned kernel for
+ * `matrix` at `rhs` (few row-owned workgroups, long rows, rhs >= 16).  No
+ * counterpart in the reference; no plan acts on it by itself. */
+inline bool split_row_advised(const Matrix& matrix, int rhs) {
+  int32_t advised = 0;
+  detail::check(vbsr_matrix_split_row_advised(matrix.handle(), rhs, &advised));
+  return advised != 0;
 }
 
 /** The split-row path (the reference's reserved Kernel::SplitRow) with a

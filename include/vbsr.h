@@ -168,16 +168,16 @@ int vbsr_matrix_row_schedule(const vbsr_matrix* matrix, vbsr_row_schedule* out);
  * kernel; VBSR_KERNEL_SPLIT_ROW (reserved and rejected in the reference,
  * plan.cpp:13-17) runs the split-row path (vbsr_launch_split_row) with a
  * workspace the plan allocates here and frees when destroyed;
- * VBSR_KERNEL_AUTO takes the split-row path for matrices whose row-owned
- * launch would leave most CUs idle while their rows are long (few block rows
- * of high degree), else the row-owned kernel.  The plan views the matrix,
- * which must outlive it. */
+ * VBSR_KERNEL_AUTO runs the row-owned kernel, as the reference's Auto does
+ * (docs/design.md:17), so a default plan owns no device memory.  The plan
+ * views the matrix, which must outlive it. */
 int vbsr_plan_create(const vbsr_matrix* matrix, const vbsr_plan_options* options, vbsr_plan** out);
 void vbsr_plan_destroy(vbsr_plan* plan);
 /* Plan::execute (vbsr.hpp:110; plan.cpp:19-22): enqueues C = A * B on
- * `stream` (0 = null stream).  Allocates nothing, also on the split-row
- * path; a split-row plan's executes share its workspace, so one plan must
- * not execute on two streams at once. */
+ * `stream` (0 = null stream).  Allocates nothing.  A row-owned plan (AUTO,
+ * ROW_OWNED) keeps no state, so its executes may run concurrently on any
+ * streams.  A split-row plan's executes share its workspace: they must not
+ * overlap in time (one stream, or events between streams). */
 int vbsr_plan_execute(const vbsr_plan* plan, const float* B, float* C, hipStream_t stream);
 /* Plan::launch_count (vbsr.hpp:112; plan.cpp:23-31): kernels enqueued by one
  * vbsr_plan_execute: 2 on the split-row path, else 1 (0 for a matrix
@@ -224,6 +224,13 @@ int vbsr_launch_row_owned_valu(const vbsr_device_view* matrix, const vbsr_row_sc
  * until this one has finished.  Any K, as for vbsr_launch_row_owned.
  * Two launches; allocates nothing. */
 int vbsr_split_row_workspace_bytes(const vbsr_matrix* matrix, int32_t rhs, int64_t* bytes);
+/* *advised = 1 when the split-row path is expected to beat the row-owned
+ * kernel for this matrix at this rhs, else 0.  The rule: the row-owned
+ * launch has fewer than 160 workgroups (most of the 256 CUs idle), its
+ * longest row has more than 16 k steps, and rhs >= 16.  Plans never act on
+ * it by themselves; a caller that wants the split asks for
+ * VBSR_KERNEL_SPLIT_ROW.  No counterpart in the reference. */
+int vbsr_matrix_split_row_advised(const vbsr_matrix* matrix, int32_t rhs, int32_t* advised);
 int vbsr_launch_split_row(const vbsr_matrix* matrix, const float* B, float* C, int32_t rhs, void* workspace,
                           int64_t workspace_bytes, hipStream_t stream);
 

@@ -11,6 +11,7 @@
 #include <cstring>
 #include <functional>
 #include <iostream>
+#include <memory>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -267,6 +268,90 @@ void run_move_tests() {
   run(before, "plan built before two moves");
 }
 
+// Plan copies share one handle (vbsr::Plan holds a shared_ptr).  The
+// reference's Plan is a stateless view (docs/design.md:15), so a default
+// plan and a copy of it may execute at once on two streams.  The matrix is
+// one where the split-row path would pay (32 block rows of degree 16), so a
+// default plan that took it would share a workspace and race here.  An
+// explicit SplitRow plan and its copy do share one: with an event after each
+// execute that the other stream waits on, their results stay exact too.
+void run_concurrent_copy_tests() {
+  vbsr::GeneratorOptions options;
+  options.block_rows = 32;
+  options.block_cols = 32;
+  options.degree = 16;
+  options.distribution = vbsr::Distribution::HighVariance;
+  options.local_columns = false;
+  options.seed = 1;
+  const vbsr::HostMatrix host = vbsr::generate(options);
+  const int rhs = 64;
+  const orc_view ov = oracle_view(host);
+  vbsr::Matrix device(host);
+  if (!vbsr::split_row_advised(device, rhs)) throw std::runtime_error("split-row not advised at 32 rows, degree 16");
+  if (vbsr::split_row_advised(device, 8)) throw std::runtime_error("split-row advised at rhs 8");
+
+  struct Side {
+    std::vector<float> input, reference, serial;
+    std::vector<double> bound;
+    hipStream_t stream{};
+  };
+  Side sides[2];
+  std::vector<std::unique_ptr<DeviceBuffer>> bs, cs;
+  for (int i = 0; i < 2; ++i) {
+    Side& s = sides[i];
+    s.input.resize(size_t(host.scalar_cols() * rhs));
+    orc_make_random_input(int64_t(s.input.size()), uint64_t(21 + i), s.input.data());
+    s.reference.resize(size_t(host.scalar_rows() * rhs));
+    s.bound.resize(s.reference.size());
+    orc_cpu_reference(&ov, s.input.data(), int64_t(s.input.size()), rhs, s.reference.data());
+    orc_abs_product_sum(&ov, s.input.data(), int64_t(s.input.size()), rhs, s.bound.data());
+    bs.push_back(std::make_unique<DeviceBuffer>(s.input.size()));
+    cs.push_back(std::make_unique<DeviceBuffer>(s.reference.size()));
+    hip_ok(hipMemcpy(bs[i]->ptr, s.input.data(), s.input.size() * sizeof(float), hipMemcpyHostToDevice), "upload B");
+    hip_ok(hipStreamCreate(&s.stream), "hipStreamCreate");
+  }
+  const auto check_plans = [&](const vbsr::Plan& plan, const vbsr::Plan& copy, bool with_events, const char* name) {
+    const vbsr::Plan* plans[2] = {&plan, &copy};
+    for (int i = 0; i < 2; ++i) {
+      cs[i]->poison();
+      plans[i]->execute(bs[i]->ptr, cs[i]->ptr, sides[i].stream);
+      hip_ok(hipStreamSynchronize(sides[i].stream), "sync");
+      sides[i].serial = cs[i]->read();
+      compare(sides[i].serial, sides[i].reference, sides[i].bound, std::string(name) + " serial");
+      cs[i]->poison();
+    }
+    hipEvent_t done[2];
+    for (auto& e : done) hip_ok(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
+    for (int round = 0; round < 20; ++round)
+      for (int i = 0; i < 2; ++i) {
+        plans[i]->execute(bs[i]->ptr, cs[i]->ptr, sides[i].stream);
+        if (with_events) {
+          hip_ok(hipEventRecord(done[i], sides[i].stream), "hipEventRecord");
+          hip_ok(hipStreamWaitEvent(sides[1 - i].stream, done[i], 0), "hipStreamWaitEvent");
+        }
+      }
+    hip_ok(hipDeviceSynchronize(), "sync");
+    for (auto& e : done) hip_ok(hipEventDestroy(e), "hipEventDestroy");
+    for (int i = 0; i < 2; ++i) {
+      const std::vector<float> out = cs[i]->read();
+      if (std::memcmp(out.data(), sides[i].serial.data(), out.size() * sizeof(float)) != 0)
+        throw std::runtime_error(std::string(name) + ": interleaved result differs from the serial run");
+      compare(out, sides[i].reference, sides[i].bound, name);
+    }
+  };
+
+  const vbsr::Plan plan(device, {rhs});  // Kernel::Auto
+  const vbsr::Plan copy = plan;
+  if (plan.launch_count() != 1 || copy.launch_count() != 1)
+    throw std::runtime_error("a default plan should run the row-owned kernel (one launch)");
+  check_plans(plan, copy, false, "default plan and its copy on two streams");
+  const vbsr::Plan split(device, {rhs, vbsr::Kernel::SplitRow});
+  const vbsr::Plan split_copy = split;
+  if (split.launch_count() != 2) throw std::runtime_error("split-row plan should take two launches");
+  check_plans(split, split_copy, true, "split-row plan and its copy, events between the streams");
+  for (Side& s : sides) hip_ok(hipStreamDestroy(s.stream), "hipStreamDestroy");
+}
+
 // tests/test_main.cpp:145-161
 int run_parameter_matrix() {
   const vbsr::Distribution distributions[] = {vbsr::Distribution::Uniform, vbsr::Distribution::LowVariance,
@@ -291,8 +376,9 @@ int main() {
   try {
     run_negative_tests();
     run_move_tests();
+    run_concurrent_copy_tests();
     const int cases = run_parameter_matrix();
-    std::cout << "PASS: negative tests + Matrix move and lifetime tests + " << cases
+    std::cout << "PASS: negative tests + Matrix move and lifetime tests + concurrent plan copies + " << cases
               << " parameter cases (MFMA plan + order-preserving kernel + rocSPARSE CSR plan + grouped "
                  "rocBLAS plan, non-default stream, NaN-poisoned C, bit-identical repeats)\n";
     return 0;

@@ -474,7 +474,7 @@ def test_split_row_reference_parameter_matrix(case):
 
 
 SPLIT_CASES = [
-    # (name, rows, degree, distribution, locality, rhs, seed, auto takes the split-row path)
+    # (name, rows, degree, distribution, locality, rhs, seed, the matrix's split rule holds)
     ("few-rows-32-n8", 32, 16, "high", "random", 8, 1, True),
     ("few-rows-32-n64", 32, 16, "high", "random", 64, 1, True),
     ("few-rows-128-n32", 128, 16, "high", "random", 32, 1, True),
@@ -486,20 +486,21 @@ SPLIT_CASES = [
 
 @pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: c[0])
 def test_split_row_against_oracle_and_auto_choice(case):
-    """Kernel::SplitRow at few rows (where Auto takes it) and at configuration 3 (where Auto does not):
-    within tolerance of the oracle and bit-stable; Auto's plan takes the expected path and gives the
-    same bits as the explicit plan of that path."""
-    name, rows, degree, distribution, locality, rhs, seed, auto_split = case
+    """Kernel::SplitRow at few rows (where the split is advised) and at configuration 3 (where it is not):
+    within tolerance of the oracle and bit-stable.  Kernel::Auto is the row-owned kernel at every shape, as
+    in the reference (docs/design.md:17): one launch, the same bits as an explicit RowOwned plan.  The
+    advice holds exactly where the matrix's rule does and rhs >= 16."""
+    name, rows, degree, distribution, locality, rhs, seed, rule = case
     note(f"split-row {name}")
     c = Case(vb.generate(rows, rows, degree, distribution, locality, seed), rhs, seed)
     split = vb.Plan(c.matrix, rhs, "split_row")
     first = c.run_plan(split)
     c.check_tolerance(first, name)
     np.testing.assert_array_equal(c.run_plan(split), first)
+    assert vb.split_row_advised(c.matrix, rhs) == (rule and rhs >= 16)
     auto = vb.Plan(c.matrix, rhs, "auto")
-    assert auto.launch_count() == (2 if auto_split else 1)
-    expected = first if auto_split else c.run_plan(vb.Plan(c.matrix, rhs, "row_owned"))
-    np.testing.assert_array_equal(c.run_plan(auto), expected)
+    assert auto.launch_count() == 1
+    np.testing.assert_array_equal(c.run_plan(auto), c.run_plan(vb.Plan(c.matrix, rhs, "row_owned")))
     split.close()
     auto.close()
     c.close()
@@ -873,33 +874,82 @@ def test_values_past_2_31_use_64_bit_offsets():
 # ---- execute is stateless: concurrent streams, graph capture ---------------
 
 def test_concurrent_executes_on_two_streams():
-    """Plan::execute keeps no state (no workspace, no atomics): two plans of one matrix run
+    """A row-owned plan keeps no state (no workspace, no atomics): two plans of one matrix run
     concurrently on two streams with their own B and C, and each matches its serial result."""
     host = vb.generate(512, 512, 8, "high", "random", 31)
     matrix = vb.Matrix(host)
     try:
-        outs = []
         runs = []
         for rhs, seed in ((32, 1), (16, 2)):
             b = torch.from_numpy(o.make_random_input(host.scalar_cols * rhs, seed)).to(DEVICE)
             c = torch.full((host.scalar_rows * rhs,), float("nan"), device=DEVICE)
             runs.append((vb.Plan(matrix, rhs), b, c, torch.cuda.Stream(device=DEVICE)))
-        serial = []
-        for plan, b, c, stream in runs:
+        interleave_and_compare(runs, events=False)
+        for plan, _, _, _ in runs:
+            plan.close()
+    finally:
+        matrix.close()
+
+
+def interleave_and_compare(runs, events, oracle_checks=None):
+    """Runs each (plan, B, C, stream) once alone, then 20 times interleaved across the streams (with an
+    event after each execute that the other stream waits on, if `events`), and checks every final C bit
+    for bit against its serial run and, where given, against the oracle."""
+    serial = []
+    for plan, b, c, stream in runs:
+        with torch.cuda.stream(stream):
+            plan.execute(b, c, stream)
+        stream.synchronize()
+        serial.append(c.cpu().numpy().copy())
+        c.fill_(float("nan"))
+    torch.cuda.synchronize()
+    for _ in range(20):
+        for i, (plan, b, c, stream) in enumerate(runs):
             with torch.cuda.stream(stream):
                 plan.execute(b, c, stream)
-            stream.synchronize()
-            serial.append(c.cpu().numpy().copy())
-            c.fill_(float("nan"))
-        torch.cuda.synchronize()
-        for _ in range(20):  # interleave many launches on both streams
-            for plan, b, c, stream in runs:
-                with torch.cuda.stream(stream):
-                    plan.execute(b, c, stream)
-        torch.cuda.synchronize()
-        for (plan, b, c, stream), expected in zip(runs, serial):
-            assert c.cpu().numpy().tobytes() == expected.tobytes()
-            plan.close()
+                if events:
+                    done = torch.cuda.Event()
+                    done.record(stream)
+                    runs[(i + 1) % len(runs)][3].wait_event(done)
+    torch.cuda.synchronize()
+    for i, ((plan, b, c, stream), expected) in enumerate(zip(runs, serial)):
+        out = c.cpu().numpy()
+        assert out.tobytes() == expected.tobytes(), f"run {i}: interleaved result differs from the serial run"
+        if oracle_checks is not None:
+            oracle_checks[i](out)
+
+
+@pytest.mark.parametrize("kernel", ["auto", "split_row"])
+def test_one_plan_on_two_streams_at_few_long_rows(kernel):
+    """32 block rows of degree 16 at RHS 64, where the split-row path is advised.  A default plan (Auto:
+    the row-owned kernel, stateless as the reference's) executes on two streams at once with different B
+    and C -- the same plan handle on both streams, as two copies of a vbsr::Plan share it -- and every
+    result equals its serial run and the oracle.  An explicit SplitRow plan shares one workspace across its
+    executes, so there the streams are ordered by events, as documented, and the results are exact too."""
+    rhs = 64
+    host = vb.generate(32, 32, 16, "high", "random", 1)
+    matrix = vb.Matrix(host)
+    try:
+        assert vb.split_row_advised(matrix, rhs)
+        plan = vb.Plan(matrix, rhs, kernel)
+        assert plan.launch_count() == (2 if kernel == "split_row" else 1)
+        oracle_host = o.HostMatrix(host.block_rows, host.block_cols, **host.arrays())
+        runs, checks = [], []
+        for seed in (21, 22):
+            b_host = o.make_random_input(host.scalar_cols * rhs, seed)
+            expected = o.cpu_reference(oracle_host, b_host, rhs)
+            bound = o.abs_product_sum(oracle_host, b_host, rhs)
+
+            def check(out, expected=expected, bound=bound, seed=seed):
+                _, rel_l2, normwise, elementwise = o.parity_errors(out, expected, bound)
+                assert normwise <= 1e-5 and rel_l2 <= 1e-5 and elementwise <= 1e-6, f"seed {seed}"
+
+            b = torch.from_numpy(b_host).to(DEVICE)
+            c = torch.full((host.scalar_rows * rhs,), float("nan"), device=DEVICE)
+            runs.append((plan, b, c, torch.cuda.Stream(device=DEVICE)))
+            checks.append(check)
+        interleave_and_compare(runs, events=kernel == "split_row", oracle_checks=checks)
+        plan.close()
     finally:
         matrix.close()
 

@@ -92,6 +92,7 @@ SIGNATURES = {
     "vbsr_launch_row_owned_valu": (ctypes.c_int, [ctypes.POINTER(DeviceView), ctypes.POINTER(RowSchedule), _P, _P,
                                                   ctypes.c_int32, _P]),
     "vbsr_split_row_workspace_bytes": (ctypes.c_int, [_P, ctypes.c_int32, ctypes.POINTER(ctypes.c_int64)]),
+    "vbsr_matrix_split_row_advised": (ctypes.c_int, [_P, ctypes.c_int32, ctypes.POINTER(ctypes.c_int32)]),
     "vbsr_launch_split_row": (ctypes.c_int, [_P, _P, _P, ctypes.c_int32, _P, ctypes.c_int64, _P]),
     "vbsr_launch_split_row_static": (ctypes.c_int, [_P, _P, _P, ctypes.c_int32, _P]),
     "vbsr_csr_plan_create": (ctypes.c_int, [ctypes.POINTER(HostView), ctypes.c_int32, ctypes.POINTER(_P)]),
@@ -365,6 +366,15 @@ def split_row_workspace_bytes(matrix, rhs):
     out = ctypes.c_int64()
     _check(library().vbsr_split_row_workspace_bytes(matrix._handle, int(rhs), ctypes.byref(out)))
     return out.value
+
+
+def split_row_advised(matrix, rhs):
+    """Whether the split-row path is expected to beat the row-owned kernel for `matrix` at `rhs` (few row-owned
+    workgroups, long rows, rhs >= 16).  Plans never act on it by themselves: Kernel::Auto is the row-owned
+    kernel, as in the reference."""
+    out = ctypes.c_int32()
+    _check(library().vbsr_matrix_split_row_advised(matrix._handle, int(rhs), ctypes.byref(out)))
+    return bool(out.value)
 
 
 def launch_split_row(matrix, B, C, rhs, workspace, workspace_bytes=None, stream=None):

@@ -66,7 +66,8 @@ def main(argv=None):
     p.add_argument("--no-cold", action="store_true", help="skip the cold-cache repetitions")
     p.add_argument("--limit", type=int, default=0, help="run only the first N cases")
     p.add_argument("--kernel", choices=["auto", "row_owned", "split_row"], default="auto",
-                   help="the plan's kernel selection (auto: the product's default)")
+                   help="the plan's kernel selection (auto, the default, is the row-owned kernel as in the "
+                        "reference; split_row rows are reported under the method name split_row)")
     p.add_argument("--exe", default=EXECUTABLE)
     args = p.parse_args(argv)
     if not os.path.exists(args.exe):

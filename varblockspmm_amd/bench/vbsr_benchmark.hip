@@ -9,8 +9,8 @@
 //                                (record, run, record, wait);
 //   useful_gflops                2 * rhs * sum(h * w) / gpu median
 //                                (benchmark.cpp:197-207);
-//   launches, workspace_bytes    kernels per run, bytes of workspace (only the
-//                                rocSPARSE plan has one).
+//   launches, workspace_bytes    kernels per run, bytes of workspace (the
+//                                rocSPARSE plan's, and a split-row plan's).
 //
 // Columns appended after the reference's: the same repetitions with a 1 GiB
 // read-only sweep before each one (inputs in HBM only), the algorithmic bytes
@@ -24,8 +24,8 @@
 // asks for the reference test's uniform [-1, 1] stream.
 //
 // Methods: row_owned_hybrid (Plan::execute with Kernel::RowOwned, the
-// reference's tuned path; --kernel auto or split_row plans with those
-// kernels instead), row_owned_scalar (launch_row_owned_scalar) and
+// reference's tuned path, or Kernel::Auto, the same kernel), split_row in its
+// place for --kernel split_row, row_owned_scalar (launch_row_owned_scalar) and
 // scalar_csr_rocsparse (ScalarCsrPlan, the counterpart of the reference's
 // scalar_csr_cusparse row) and slot_grouped_rocblas (GroupedGemmPlan, the
 // counterpart of slot_grouped_cublas).
@@ -278,11 +278,14 @@ int run(const Arguments& a) {
               << (t.cold_median > 0 ? bytes / (t.cold_median * 1e6) : 0.0) << ',' << (t.identical ? 1 : 0) << '\n'
               << std::flush;
   };
-  // A split-row plan (two launches) owns the workspace the split-row path needs.
-  const size_t plan_workspace =
-      plan.launch_count() == 2 ? size_t(vbsr::split_row_workspace_bytes(matrix, a.rhs_width)) : 0;
-  report("row_owned_hybrid", bench.time([&](hipStream_t s) { plan.execute(b, c, s); }, a, c, c_count),
-         plan.launch_count(), plan_workspace);
+  // A split-row plan (two launches) owns the workspace the split-row path
+  // needs, and is reported under a method name of its own, so that its rows
+  // never mix into the reference's row_owned_hybrid column.
+  const bool split_row = kernel == vbsr::Kernel::SplitRow;
+  const size_t plan_workspace = split_row ? size_t(vbsr::split_row_workspace_bytes(matrix, a.rhs_width)) : 0;
+  report(split_row ? "split_row" : "row_owned_hybrid",
+         bench.time([&](hipStream_t s) { plan.execute(b, c, s); }, a, c, c_count), plan.launch_count(),
+         plan_workspace);
   report("row_owned_scalar",
          bench.time([&](hipStream_t s) { vbsr::launch_row_owned_scalar(view, b, c, a.rhs_width, s); }, a, c,
                     c_count),

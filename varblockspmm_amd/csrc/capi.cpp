@@ -188,6 +188,15 @@ int vbsr_split_row_workspace_bytes(const vbsr_matrix* matrix, int32_t rhs, int64
   });
 }
 
+int vbsr_matrix_split_row_advised(const vbsr_matrix* matrix, int32_t rhs, int32_t* advised) {
+  return guarded([&] {
+    require(matrix, "matrix");
+    require(advised, "advised");
+    if (!vbsr_amd::supported_rhs(rhs)) throw std::invalid_argument("unsupported rhs width");
+    *advised = vbsr_amd::split_row_advised(matrix->device.split(), rhs) ? 1 : 0;
+  });
+}
+
 int vbsr_launch_split_row(const vbsr_matrix* matrix, const float* B, float* C, int32_t rhs, void* workspace,
                           int64_t workspace_bytes, hipStream_t stream) {
   return guarded([&] {

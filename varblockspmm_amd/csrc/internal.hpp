@@ -117,8 +117,9 @@ struct HostSchedule {
   std::vector<WaveItem> rows_rhs64; // workgroups packed at kPackStepsRhs64, in the rows_wide order, for RHS 64
   int64_t groups_rhs64{};
   HostSplitSchedule split;
-  // Whether Plan's automatic choice takes the split-row path: the row-owned
-  // launch would leave most CUs idle while its rows are long.
+  // Whether the split-row path pays off for this matrix at RHS 16 and up:
+  // the row-owned launch would leave most CUs idle while its rows are long.
+  // Advice for the caller (split_row_advised); no plan switches by itself.
   bool split_preferred{};
 };
 
@@ -219,6 +220,11 @@ void launch_row_owned_valu(const vbsr_device_view& a, const vbsr_row_schedule& s
 // the caller's (a plan's own, or any buffer of at least that size that does
 // not overlap B or C).  Any K, as for launch_row_owned.
 int64_t split_workspace_floats(const DeviceMatrix::Split& split, int rhs);
+// Whether the split-row path is expected to beat the row-owned launch for
+// this matrix at this width: the schedule's rule (few row-owned workgroups,
+// long rows), at RHS 16 and up only -- at RHS 8 the split was measured 3-7%
+// slower at 64 and 128 block rows of degree 16.
+inline bool split_row_advised(const DeviceMatrix::Split& split, int rhs) { return split.preferred && rhs >= 16; }
 void launch_split_row(const vbsr_device_view& a, const vbsr_row_schedule& schedule, const DeviceMatrix::Split& split,
                       const float* b, float* c, int rhs, float* workspace, int64_t workspace_floats,
                       hipStream_t stream);

@@ -9,12 +9,17 @@
 // counterpart.  The matrix's row schedule (schedule.cpp) orders and places
 // the rows instead.
 //
+// Kernel::Auto and Kernel::RowOwned both run the row-owned kernel, as in the
+// reference (docs/design.md:15,17): the plan views the matrix, owns nothing,
+// and its executes may run concurrently on any streams.
+//
 // Kernel::SplitRow, reserved in the reference (plan.cpp:13-17), is the
-// split-row path here: each row's k steps are cut into parts computed by the
-// same kernel into a plan-owned workspace, and a second launch sums each
-// row's parts in a fixed order.  Kernel::Auto takes it for matrices whose
-// row-owned launch would leave most CUs idle while their rows are long (few
-// block rows of high degree); Kernel::RowOwned never does.
+// split-row path here, taken only on request: each row's k steps are cut
+// into parts computed by the same kernel into a plan-owned workspace, and a
+// second launch sums each row's parts in a fixed order.  Such a plan's
+// executes share that workspace.  The matrix reports whether the split pays
+// for a given width (vbsr_matrix_split_row_advised); the plan never switches
+// by itself.
 //
 // Every K stays on the MFMA kernel: past the reach of its 32-bit B offsets
 // (K > 153,391,684 at RHS 8, K > 71,582,785 otherwise) it addresses B with
@@ -30,7 +35,7 @@ Plan::Plan(const DeviceMatrix& matrix, const vbsr_plan_options& o)
   if (!supported_rhs(o.rhs_width)) throw std::invalid_argument("rhs_width must be 8,16,32,64");
   if (o.kernel != VBSR_KERNEL_AUTO && o.kernel != VBSR_KERNEL_ROW_OWNED && o.kernel != VBSR_KERNEL_SPLIT_ROW)
     throw std::invalid_argument("unknown kernel selection");
-  split_row_ = o.kernel == VBSR_KERNEL_SPLIT_ROW || (o.kernel == VBSR_KERNEL_AUTO && split_.preferred);
+  split_row_ = o.kernel == VBSR_KERNEL_SPLIT_ROW;
   if (split_row_) {
     workspace_floats_ = split_workspace_floats(split_, o.rhs_width);
     if (workspace_floats_ > 0)
