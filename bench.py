@@ -53,11 +53,14 @@ def parse():
     p.add_argument("--locality", default="random")
     p.add_argument("--rhs", type=int, default=32)
     p.add_argument("--seed", type=int, default=1)
-    p.add_argument("--kernel", choices=["plan", "scalar", "valu", "wide_b"], default="plan",
+    p.add_argument("--kernel", choices=["plan", "scalar", "valu", "wide_b", "rhs64_splitk", "rhs64_tiles"],
+                   default="plan",
                    help="plan = the library's Plan::execute; scalar = the order-preserving kernel; valu = the "
                         "row-owned kernel with plain FP32 multiply-adds instead of MFMA (the measured alternative); "
                         "wide_b = the row-owned kernel reading B through 64-bit addresses, the form it takes past "
-                        "the 32-bit offset bound on K")
+                        "the 32-bit offset bound on K; rhs64_splitk / rhs64_tiles = launch_row_owned with the RHS 64 "
+                        "kernel forced to the split-k kernel / the tile split (the plan takes the one the matrix's "
+                        "rule names)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-parity", action="store_true")
     p.add_argument("--calibrate-copy-mib", type=int, default=0,
@@ -218,6 +221,8 @@ def main():
     torch.cuda.synchronize()
 
     schedule = matrix.row_schedule()
+    if args.kernel in ("rhs64_splitk", "rhs64_tiles"):
+        schedule.rhs64_tiles = 1 if args.kernel == "rhs64_tiles" else 0
 
     def step():
         if args.kernel == "plan":
@@ -226,6 +231,8 @@ def main():
             vb.launch_row_owned_valu(view, schedule, b_dev, c_dev, args.rhs, stream)
         elif args.kernel == "wide_b":
             vb.launch_row_owned_wide_b(view, schedule, b_dev, c_dev, args.rhs, stream)
+        elif args.kernel in ("rhs64_splitk", "rhs64_tiles"):
+            vb.launch_row_owned(view, schedule, b_dev, c_dev, args.rhs, stream)
         else:
             vb.launch_row_owned_scalar(view, b_dev, c_dev, args.rhs, stream)
 
@@ -356,7 +363,8 @@ def main():
         "vs_baseline": round(ref_ms / median, 3) if (ref_ms and args.kernel == "plan") else None,
         "dtype": "f32",
         "data": "synthetic (seeded generator, B = mt19937 uniform[-1,1])",
-        "config": {"workload": workload, "kernel": args.kernel, "sum_hw": work["sum_hw"],
+        "config": {"workload": workload, "kernel": args.kernel, "rhs64_tiles": int(matrix.row_schedule().rhs64_tiles),
+                   "sum_hw": work["sum_hw"],
                    "algorithmic_bytes": work["bytes"], "flops": work["flops"], "launches": plan.launch_count(),
                    "timing": "hipEventDisableSystemFence events on the kernel's stream, each step synchronised "
                              "before the next (as bench/benchmark.cpp:148-183); cold = 1 GiB read-only sweep before "

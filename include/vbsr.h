@@ -160,6 +160,15 @@ typedef struct vbsr_row_schedule {
   const void* rows_wide;  /* device: the same row items, launch order for rhs 32 */
   const void* rows_rhs64; /* device: row items for rhs 64, which packs longer light rows */
   int64_t groups_rhs64;   /* workgroups of a launch from rows_rhs64 */
+  const void* rows_tile;  /* device: row items of the rhs 64 tile split, one row per workgroup */
+  int64_t groups_tile;    /* workgroups of a launch from rows_tile */
+  /* Which kernel an rhs 64 launch runs: 0 the split-k kernel over rows_rhs64
+   * (a row's k steps shared by four waves, each with all four 16-column RHS
+   * tiles), 1 the tile split over rows_tile (four waves on one row, each
+   * with one RHS tile over all the row's steps).  vbsr_matrix_create sets it
+   * by the matrix's rule; both kernels are correct for any matrix, so a
+   * caller may set either value in its copy of the struct. */
+  int32_t rhs64_tiles;
 } vbsr_row_schedule;
 int vbsr_matrix_row_schedule(const vbsr_matrix* matrix, vbsr_row_schedule* out);
 

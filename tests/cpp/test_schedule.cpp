@@ -249,6 +249,22 @@ void check_split(const vbsr_host_view& m, const vbsr_amd::HostSchedule& s) {
   CHECK(s.split_preferred == (units < 160 && longest > 2 * kRowWaves * vbsr_amd::kStepRun));
 }
 
+// The RHS 64 kernel choice, recomputed from the matrix alone: the tile split
+// runs when the longest row's k steps are at most 3 x (all steps) / (256 x 6).
+bool expected_tiles(const vbsr_host_view& m) {
+  int64_t total = 0, longest = 0;
+  for (int32_t i = 0; i < m.block_rows; ++i) {
+    int64_t steps = 0;
+    for (int32_t blk = m.row_ptr[i]; blk < m.row_ptr[i + 1]; ++blk) {
+      const int32_t w = m.col_size[m.block_col[blk]];
+      steps += w / 16 + (w % 16 != 0);
+    }
+    total += steps;
+    longest = std::max(longest, steps);
+  }
+  return m.block_rows > 0 && longest * 256 * 6 <= 3 * total;
+}
+
 bool same(const std::vector<vbsr_amd::WaveItem>& a, const std::vector<vbsr_amd::WaveItem>& b) {
   return a.size() == b.size() && (a.empty() || std::memcmp(a.data(), b.data(), a.size() * sizeof(a[0])) == 0);
 }
@@ -266,12 +282,16 @@ void check_view(const vbsr_host_view& m, const char* name, double max_seconds, b
   }
   check_steps(m, s);
   check_split(m, s);
+  CHECK(s.rhs64_tiles == expected_tiles(m));
   std::vector<int> xcd_of_row(size_t(m.block_rows), -1);
   check_order(m, s, s.rows, xcd_of_row, false, s.groups, vbsr_amd::kPackSteps);
   check_order(m, s, s.rows_wide, xcd_of_row, true, s.groups, vbsr_amd::kPackSteps);
   // The RHS 64 order packs more rows, so it places its own workgroups.
   std::vector<int> xcd_of_row64(size_t(m.block_rows), -1);
   check_order(m, s, s.rows_rhs64, xcd_of_row64, true, s.groups_rhs64, vbsr_amd::kPackStepsRhs64);
+  // The tile split's order gives every row with steps a workgroup of its own.
+  std::vector<int> xcd_of_row_tile(size_t(m.block_rows), -1);
+  check_order(m, s, s.rows_tile, xcd_of_row_tile, true, s.groups_tile, 0);
   // Up to 192 workgroups per XCD the wide order is the heaviest-first one;
   // above it, on a random matrix, the chain reorders them.
   int64_t units = 0;
@@ -283,6 +303,7 @@ void check_view(const vbsr_host_view& m, const char* name, double max_seconds, b
   }
   const vbsr_amd::HostSchedule again = vbsr_amd::build_schedule(m);
   if (!(same(s.rows, again.rows) && same(s.rows_wide, again.rows_wide) && same(s.rows_rhs64, again.rows_rhs64) &&
+        same(s.rows_tile, again.rows_tile) &&
         same(s.split.items, again.split.items) &&
         s.steps.size() == again.steps.size())) {
     std::fprintf(stderr, "FAILED: schedule not deterministic\n");
@@ -403,6 +424,30 @@ int main() {
     check_host(vbsr_amd::generate(options), name, shape[0] == 4096 && shape[2] >= 8);
   }
   check_host(with_empty_row(), "hand-made, empty middle row");
+  // The RHS 64 rule on shapes it was measured on: the tile split at 4096
+  // block rows of degree 1 to 16 and at 1024 rows of degree 16; the split-k
+  // kernel at 256 and 512 rows of degree 16 (a few long rows per CU).
+  const int32_t tile_shapes[][5] = {
+      // rows, degree, distribution, seed, expected
+      {4096, 8, VBSR_DIST_HIGH_VARIANCE, 1, 1}, {4096, 16, VBSR_DIST_BIMODAL_8_OR_64, 3, 1},
+      {1024, 16, VBSR_DIST_HIGH_VARIANCE, 1, 1}, {256, 16, VBSR_DIST_HIGH_VARIANCE, 1, 0},
+      {512, 16, VBSR_DIST_HIGH_VARIANCE, 1, 0}, {4096, 2, VBSR_DIST_HIGH_VARIANCE, 1, 1},
+      {4096, 1, VBSR_DIST_HIGH_VARIANCE, 1, 1}};
+  for (const auto& t : tile_shapes) {
+    vbsr_generator_options options{};
+    options.block_rows = options.block_cols = t[0];
+    options.degree = t[1];
+    options.rhs_width = 64;
+    options.distribution = t[2];
+    options.locality = VBSR_LOCALITY_RANDOM;
+    options.seed = uint64_t(t[3]);
+    const vbsr_amd::HostMatrix host = vbsr_amd::generate(options);
+    const vbsr_amd::HostSchedule s = vbsr_amd::build_schedule(host.view());
+    if (s.rhs64_tiles != (t[4] != 0)) {
+      std::fprintf(stderr, "FAILED: rhs64_tiles=%d at rows=%d degree=%d\n", int(s.rhs64_tiles), t[0], t[1]);
+      ++failures;
+    }
+  }
   check_shared_columns(16384, 8, 8);
   check_shared_columns(65536, 16384, 16);
   check_panel_ranges();

@@ -390,6 +390,61 @@ def test_wide_b_addressing_is_bit_identical(name, rhs):
     c.close()
 
 
+@pytest.mark.parametrize("tiles", [0, 1], ids=["split-k", "tile-split"])
+@pytest.mark.parametrize("name", list(WIDE_B_MATRICES))
+def test_rhs64_kernels_on_edge_matrices(name, tiles):
+    """RHS 64 with each of its two kernels forced through the schedule's rhs64_tiles field (the
+    matrix's rule picks one; both must be right for any matrix): within tolerance of the oracle, empty
+    rows zero, bit-identical across runs, and the 64-bit B form bit-identical to the offset form, also
+    with +Inf where the upper lanes of a half step would read."""
+    rhs = 64
+    note(f"rhs64 kernel tiles={tiles} {name}")
+    host = WIDE_B_MATRICES[name]()
+    c = Case(host, rhs, 29)
+    view, schedule = c.matrix.device_view(), c.matrix.row_schedule()
+    schedule.rhs64_tiles = tiles
+    narrow = lambda: vb.launch_row_owned(view, schedule, c.b_dev, c.c_dev, rhs, c.stream)
+    first = c.run(narrow)
+    c.check_tolerance(first, f"{name} tiles={tiles}")
+    out = first.reshape(rhs, host.scalar_rows)
+    for i in np.nonzero(np.diff(host.row_ptr) == 0)[0]:
+        assert np.all(out[:, host.row_scalar_off[i]:host.row_scalar_off[i + 1]] == 0.0)
+    assert c.run(narrow).tobytes() == first.tobytes(), "not bit-identical across runs"
+    wide = c.run(lambda: vb.launch_row_owned_wide_b(view, schedule, c.b_dev, c.c_dev, rhs, c.stream))
+    assert wide.tobytes() == first.tobytes(), "wide B differs"
+    b = c.b.reshape(rhs, host.scalar_cols).copy()
+    for col in range(1, host.block_cols, 2):
+        start = int(host.col_scalar_off[col])
+        b[:, start:start + 8] = np.inf
+    c.b_dev = torch.from_numpy(b.reshape(-1).copy()).to(DEVICE)
+    assert c.run(narrow).tobytes() == c.run(
+        lambda: vb.launch_row_owned_wide_b(view, schedule, c.b_dev, c.c_dev, rhs, c.stream)).tobytes()
+    c.close()
+
+
+@pytest.mark.parametrize("shape", [(4096, 8, "high", 1, 1), (256, 16, "high", 1, 0)], ids=["4096-d8", "256-d16"])
+def test_rhs64_plan_takes_the_rule_kernel(shape):
+    """The plan's RHS 64 launch is the kernel the matrix's rule names (the tile split at 4096 block rows of
+    degree 8, the split-k kernel at 256 rows of degree 16): bit-identical to launch_row_owned with that
+    kernel forced, within tolerance of the oracle, and within tolerance of the other kernel."""
+    rows, degree, distribution, seed, expected = shape
+    note(f"rhs64 rule {shape}")
+    c = Case(vb.generate(rows, rows, degree, distribution, "random", seed), 64, seed)
+    schedule = c.matrix.row_schedule()
+    assert schedule.rhs64_tiles == expected
+    planned = c.run_plan(vb.Plan(c.matrix, 64))
+    c.check_tolerance(planned, f"plan {shape}")
+    view = c.matrix.device_view()
+    for tiles in (0, 1):
+        schedule.rhs64_tiles = tiles
+        forced = c.run(lambda: vb.launch_row_owned(view, schedule, c.b_dev, c.c_dev, 64, c.stream))
+        if tiles == expected:
+            assert forced.tobytes() == planned.tobytes()
+        else:
+            c.check_tolerance(forced, f"forced tiles={tiles} {shape}")
+    c.close()
+
+
 @pytest.mark.parametrize("rhs", [8, 16, 32, 64])
 def test_unused_b_entries_never_reach_c(rhs):
     """NaN in every B row that no block references (including the rows right

@@ -56,7 +56,8 @@ class GeneratorOptions(ctypes.Structure):
 class RowSchedule(ctypes.Structure):
     _fields_ = [("steps", ctypes.c_void_p), ("rows", ctypes.c_void_p), ("groups", ctypes.c_int64),
                 ("step_limit", ctypes.c_int32), ("rows_wide", ctypes.c_void_p), ("rows_rhs64", ctypes.c_void_p),
-                ("groups_rhs64", ctypes.c_int64)]
+                ("groups_rhs64", ctypes.c_int64), ("rows_tile", ctypes.c_void_p), ("groups_tile", ctypes.c_int64),
+                ("rhs64_tiles", ctypes.c_int32)]
 
 
 class PlanOptions(ctypes.Structure):

@@ -61,6 +61,9 @@ DeviceMatrix::DeviceMatrix(const vbsr_host_view& host) {
     schedule_.groups = schedule.groups;
     schedule_.rows_rhs64 = upload(schedule.rows_rhs64.data(), int64_t(schedule.rows_rhs64.size()), allocations_);
     schedule_.groups_rhs64 = schedule.groups_rhs64;
+    schedule_.rows_tile = upload(schedule.rows_tile.data(), int64_t(schedule.rows_tile.size()), allocations_);
+    schedule_.groups_tile = schedule.groups_tile;
+    schedule_.rhs64_tiles = schedule.rhs64_tiles ? 1 : 0;
     schedule_.step_limit = int32_t(std::max<size_t>(schedule.steps.size(), 1) - 1);
     split_.items = upload(schedule.split.items.data(), int64_t(schedule.split.items.size()), allocations_);
     split_.rows = upload(schedule.split.rows.data(), int64_t(schedule.split.rows.size()), allocations_);

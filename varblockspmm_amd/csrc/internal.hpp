@@ -116,6 +116,16 @@ struct HostSchedule {
   int64_t groups{};                 // workgroups of a launch from rows or rows_wide (multiple of kXcds)
   std::vector<WaveItem> rows_rhs64; // workgroups packed at kPackStepsRhs64, in the rows_wide order, for RHS 64
   int64_t groups_rhs64{};
+  // The tile-split kernel's order for RHS 64: every row with k steps a
+  // workgroup of its own (empty rows packed kRowWaves to one), placed and
+  // chained like the other orders.
+  std::vector<WaveItem> rows_tile;
+  int64_t groups_tile{};
+  // Whether RHS 64 runs the tile-split kernel over rows_tile instead of the
+  // split-k kernel over rows_rhs64: a row's steps then run one after another
+  // on one workgroup, so the longest row must stay within kTileSpanLimit
+  // times the mean steps per workgroup slot.
+  bool rhs64_tiles{};
   HostSplitSchedule split;
   // Whether the split-row path pays off for this matrix at RHS 16 and up:
   // the row-owned launch would leave most CUs idle while its rows are long.

@@ -526,35 +526,191 @@ __global__ __launch_bounds__(kThreads) void row_owned_mfma_kernel(Launch L) {
   }
 }
 
+// RHS 64 tile split (row_tiles_kernel).  A workgroup takes one block row
+// (the schedule's tile order gives every row with k steps a workgroup of its
+// own and packs only empty rows, four to a workgroup, which it takes one
+// after another), and all four waves work on it: wave w computes RHS tile w
+// (C columns 16 w .. 16 w + 15) over all of the row's k steps, in step
+// order.
+// A step's A tile (16 block columns, 64 h bytes) is loaded once for the
+// workgroup, 16 bytes per lane, into one of two LDS buffers, and one barrier
+// per step publishes it; each wave moves its own B tile through its own LDS
+// slot.  There is no cross-wave reduction, and a wave holds T row tiles of
+// one RHS tile: a quarter of the split-k kernel's accumulators, so a SIMD
+// holds 6 of these waves against 3 of the split-k kernel's.  The price is
+// that a row's steps run one after another on one workgroup, so the launch
+// is as long as its longest row; the schedule takes this kernel only where
+// that stays short against the work per workgroup slot (rhs64_tiles).
+constexpr int kTileLd = 16 * kMaxTiles + 4;  // A buffer: float (r, k) at k * kTileLd + r
+constexpr int kTileFloats = 16 * kTileLd;
+constexpr int kTileLdsBytes = 2 * kTileFloats * 4 + kWaves * kWave * 16;
+
+template <int T, bool kWideB>
+__device__ __forceinline__ void tile_row(const Launch& L, const WaveItem& item, char* lds, int wave, int lane) {
+  constexpr int ld = kTileLd;
+  const int tid = wave * kWave + lane;
+  const int group = lane >> 4;
+  const int x = lane & 15;
+  const int h = uniform(item.h);
+  const int count = uniform(item.step_count);
+  const int first = uniform(item.step_first);
+  const int last_rows = h - 16 * (T - 1);
+  const uint32_t ldb = uint32_t(L.a.scalar_cols);
+  float* a_bufs = reinterpret_cast<float*>(lds);
+  f32x4* b_slot = reinterpret_cast<f32x4*>(lds + 2 * kTileFloats * 4) + wave * kWave;
+
+  // This thread's 16 bytes of the step's column-major h x 16 A tile go to
+  // float (k, r) of the buffer (f / h computed as in row_body); threads past
+  // the tile hold zeros and write them to the never-read padding rows.
+  const uint32_t h_recip = uint32_t(uniform(int((65536u + uint32_t(h) - 1u) / uint32_t(h))));
+  const int f = 4 * tid;
+  const int fk = int((uint32_t(f) * h_recip) >> 16);
+  const int a_write = f < 16 * h ? fk * ld + (f - fk * h) : (tid & 15) * ld + 16 * kMaxTiles;
+  const int a_read = 4 * group * ld + x;
+  const int a_read_last = 4 * group * ld + 16 * (T - 1) + (x & (last_rows - 1));
+  const uint32_t a_full_bytes = uint32_t(16 * h) * 4u;
+  const uint32_t a_half_bytes = uint32_t(8 * h) * 4u;
+
+  // B: lane 4n + q of wave w reads B[k0 + 4q .. k0 + 4q + 3, 16 w + n], as
+  // one tile of the split-k kernel.
+  const int b_n = lane >> 2;
+  const int b_q = lane & 3;
+  const uint32_t b_full = uint32_t(b_n) * ldb * 4u + uint32_t(16 * b_q);
+  const uint32_t b_half = b_q < 2 ? b_full : kOutOfRange;
+  const uint32_t b_span = 15u * ldb * 4u;
+  const int64_t b_lane = int64_t(b_n) * L.a.scalar_cols + 4 * b_q;  // kWideB: the lane's float offset
+  const int slot_write = b_slot_index(b_n, b_q);
+  const int slot_read = b_slot_index(x, group);
+
+  f32x4 acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  struct TileStage {
+    f32x4 a, b;
+  };
+  int parity = 0;  // A buffer of the next step
+  for (int seg = 0; seg < count; seg += kWave) {
+    const int seg_count = min(kWave, count - seg);
+    const StepRec rec = L.steps[min(first + seg + min(lane, seg_count - 1), L.step_limit)];
+    auto issue = [&](TileStage& st, int j) {
+      const bool live = j < seg_count;
+      const int l = min(j, kWave - 1);
+      const int64_t a_off = lane_value(rec.a_off, l);
+      const int64_t b_word = lane_value(rec.b_off, l);
+      const bool half = (b_word & kHalfStep) != 0;
+      const rsrc_t a_rsrc = make_rsrc(L.a.values + a_off, live ? (half ? a_half_bytes : a_full_bytes) : 0u);
+      st.a = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, 16 * tid, 0, kNonTemporal));
+      const float* b_base = L.b + (b_word & kOffsetMask) + int64_t(wave) * 16 * L.a.scalar_cols;
+      if constexpr (kWideB) {
+        st.b = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (live && (!half || b_q < 2)) st.b = *reinterpret_cast<const f32x4_unaligned*>(b_base + b_lane);
+      } else {
+        const rsrc_t b_rsrc = make_rsrc(b_base, live ? b_span + (half ? 32u : 64u) : 0u);
+        st.b = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, int(half ? b_half : b_full), 0, 0));
+      }
+    };
+    // Writes the step's A quarter and B tile, publishes the A tile with one
+    // barrier, runs the wave's T x 4 MFMAs.  The two A buffers alternate: a
+    // wave writes buffer p only after the barrier of the step before, which
+    // every wave reaches after its reads of buffer p two steps back.
+    auto compute = [&](const TileStage& st) {
+      float* a = a_bufs + parity * kTileFloats;
+      parity ^= 1;
+      *reinterpret_cast<f32x4*>(a + a_write) = st.a;
+      b_slot[slot_write] = st.b;
+      __syncthreads();
+      const f32x4 bv = b_slot[slot_read];
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float av = t < T - 1 ? a[a_read + 16 * t + i * ld] : a[a_read_last + i * ld];
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[i], av, acc[t], 0, 0, 0);
+        }
+    };
+    // Two stages, as in row_body: step j + 1 loads while step j computes; an
+    // odd count ends on a dead step (zero-byte loads, zeros multiplied in).
+    TileStage r0, r1;
+    issue(r0, 0);
+    for (int j = 0; j < seg_count; j += 2) {
+      issue(r1, j + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(r0);
+      issue(r0, j + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(r1);
+    }
+  }
+  // Every wave's reads of this row's A buffers end before the next row of
+  // the unit writes one.
+  __syncthreads();
+  const int64_t ldc = L.ldc;
+  float* c_row = L.c + item.c_off + x;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    if (t < T - 1 || x < last_rows) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) c_row[16 * t + int64_t(wave * 16 + 4 * group + v) * ldc] = acc[t][v];
+    }
+  }
+}
+
+template <bool kWideB>
+__global__ __launch_bounds__(kThreads) void row_tiles_kernel(Launch L) {
+  __shared__ __attribute__((aligned(16))) char lds[kTileLdsBytes];
+  const int wave = uniform(int(threadIdx.x) / kWave);
+  const int lane = int(threadIdx.x) % kWave;
+  const WaveItem* unit = L.items + int64_t(blockIdx.x) * kWaves;
+  // Every wave reads the same items, so every branch below is uniform across
+  // the workgroup and every wave reaches every barrier.
+  const bool shared = uniform(unit[0].group) > 1;
+  const int rows = shared ? 1 : kWaves;
+  for (int r = 0; r < rows; ++r) {
+    const WaveItem item = unit[r];
+    if (uniform(item.step_count) < 0) continue;
+    switch ((uniform(item.h) + 15) >> 4) {
+    case 1: tile_row<1, kWideB>(L, item, lds, wave, lane); break;
+    case 2: tile_row<2, kWideB>(L, item, lds, wave, lane); break;
+    case 3: tile_row<3, kWideB>(L, item, lds, wave, lane); break;
+    default: tile_row<4, kWideB>(L, item, lds, wave, lane); break;
+    }
+  }
+}
+
+// tiles: RHS 64 runs the tile-split kernel (the MFMA kernel only).
 template <int RHS, bool kValu, bool kWideB>
-void launch(const Launch& L, int64_t groups, hipStream_t stream) {
-  row_owned_mfma_kernel<RHS, kValu, kWideB><<<dim3(unsigned(groups)), dim3(kThreads), 0, stream>>>(L);
+void launch(const Launch& L, int64_t groups, bool tiles, hipStream_t stream) {
+  if (RHS == 64 && !kValu && tiles)
+    row_tiles_kernel<kWideB><<<dim3(unsigned(groups)), dim3(kThreads), 0, stream>>>(L);
+  else
+    row_owned_mfma_kernel<RHS, kValu, kWideB><<<dim3(unsigned(groups)), dim3(kThreads), 0, stream>>>(L);
 }
 
 template <bool kValu, bool kWideB>
-void launch_rhs(const Launch& L, int64_t groups, int rhs, hipStream_t stream) {
+void launch_rhs(const Launch& L, int64_t groups, int rhs, bool tiles, hipStream_t stream) {
   switch (rhs) {
-  case 8: launch<8, kValu, kWideB>(L, groups, stream); break;
-  case 16: launch<16, kValu, kWideB>(L, groups, stream); break;
-  case 32: launch<32, kValu, kWideB>(L, groups, stream); break;
-  default: launch<64, kValu, kWideB>(L, groups, stream); break;
+  case 8: launch<8, kValu, kWideB>(L, groups, false, stream); break;
+  case 16: launch<16, kValu, kWideB>(L, groups, false, stream); break;
+  case 32: launch<32, kValu, kWideB>(L, groups, false, stream); break;
+  default: launch<64, kValu, kWideB>(L, groups, tiles, stream); break;
   }
 }
 
 // wide: 64-bit B addressing (the MFMA kernel only; the VALU variant keeps
 // the 32-bit offset bound).
 template <bool kValu>
-void launch_items(const Launch& L, int64_t groups, int rhs, bool wide, hipStream_t stream) {
+void launch_items(const Launch& L, int64_t groups, int rhs, bool wide, bool tiles, hipStream_t stream) {
   if (groups <= 0) return;
   if (groups > int64_t(0x7fffffff)) throw std::invalid_argument("schedule too large for one launch");
   if constexpr (kValu) {
     if (wide) throw std::invalid_argument("the VALU variant needs (min(rhs, 16) - 1) * K * 4 + 128 <= 0xfffffff0");
-    launch_rhs<true, false>(L, groups, rhs, stream);
+    launch_rhs<true, false>(L, groups, rhs, false, stream);
   } else {
     if (wide)
-      launch_rhs<false, true>(L, groups, rhs, stream);
+      launch_rhs<false, true>(L, groups, rhs, tiles, stream);
     else
-      launch_rhs<false, false>(L, groups, rhs, stream);
+      launch_rhs<false, false>(L, groups, rhs, tiles, stream);
   }
   check_hip(hipGetLastError(), "row_owned_mfma launch");
 }
@@ -633,13 +789,20 @@ void launch_row_owned_math(const vbsr_device_view& a, const vbsr_row_schedule& s
   check_panels(a, b, c, rhs);
   const void* rows = rhs >= 32 && s.rows_wide != nullptr ? s.rows_wide : s.rows;
   int64_t groups = s.groups;
-  if (rhs == 64 && s.rows_rhs64 != nullptr) {
+  const bool tiles = !kValu && rhs == 64 && s.rhs64_tiles != 0;
+  if (tiles) {
+    if (s.rows_tile == nullptr && s.groups_tile > 0) throw std::invalid_argument("schedule without a tile order");
+    rows = s.rows_tile;
+    groups = s.groups_tile;
+  } else if (rhs == 64 && s.rows_rhs64 != nullptr) {
     rows = s.rows_rhs64;
     groups = s.groups_rhs64;
   }
   const Launch L{a, static_cast<const StepRec*>(s.steps), static_cast<const WaveItem*>(rows), s.step_limit, b, c,
                  a.scalar_rows};
-  launch_items<kValu>(L, groups, rhs, wide_b || !narrow_b_offsets(a, rhs), stream);
+  // At RHS 64 the schedule says which kernel runs: the split-k kernel or
+  // the tile split (rhs64_tiles, set by the matrix's rule).
+  launch_items<kValu>(L, groups, rhs, wide_b || !narrow_b_offsets(a, rhs), tiles, stream);
 }
 
 }  // namespace
@@ -677,7 +840,7 @@ void launch_split_row(const vbsr_device_view& a, const vbsr_row_schedule& s, con
   if (a.block_rows <= 0) return;
   const Launch L{a, static_cast<const StepRec*>(s.steps), split.items, s.step_limit, b, workspace,
                  split.virtual_rows};
-  launch_items<false>(L, split.groups, rhs, !narrow_b_offsets(a, rhs), stream);
+  launch_items<false>(L, split.groups, rhs, !narrow_b_offsets(a, rhs), false, stream);
   // A row's slab holds at most 64 * rhs elements.
   const unsigned chunks = unsigned((64 * rhs + kReduceThreads - 1) / kReduceThreads);
   split_reduce_kernel<<<dim3(unsigned(a.block_rows), chunks), dim3(kReduceThreads), 0, stream>>>(

@@ -249,6 +249,28 @@ HostSchedule build_schedule(const vbsr_host_view& m) {
   out.groups = launch_orders(kPackSteps, &out.rows, &out.rows_wide, &n_units);
   out.groups_rhs64 = launch_orders(kPackStepsRhs64, nullptr, &out.rows_rhs64, nullptr);
 
+  // The tile-split kernel's order: pack_steps 0 gives every row with k steps
+  // a workgroup of its own.
+  out.groups_tile = launch_orders(0, nullptr, &out.rows_tile, nullptr);
+
+  // RHS 64 kernel choice.  The tile-split kernel runs a row's steps one after
+  // another on one workgroup (all four waves on each step), so its launch
+  // lasts at least the longest row's steps.  It is taken when those stay
+  // within kTileSpanLimit times the mean steps per workgroup slot (6
+  // workgroups on each of the 256 CUs).  Measured against the split-k kernel
+  // at RHS 64 (cold, alternating on one box): 4096 block rows of degree 1, 2,
+  // 4, 8 and 16 and 1024-2048 rows of degree 8 and 16 (span ratio up to 2.2),
+  // 2-15% faster; 512 and 256 rows of degree 16 (ratio 3.9 and 7.8) 8% and
+  // 22% slower.
+  {
+    constexpr int64_t kTileSlots = 256 * 6;
+    constexpr int64_t kTileSpanLimit = 3;
+    int64_t longest = 0;
+    for (int32_t i = 0; i < rows; ++i) longest = std::max<int64_t>(longest, steps_of(i));
+    const int64_t total = int64_t(out.steps.size());
+    out.rhs64_tiles = rows > 0 && longest * kTileSlots <= kTileSpanLimit * total;
+  }
+
   // Split-row schedule.  Parts of a row hold part_steps consecutive steps (a
   // multiple of one run per wave, sized so that the parts of the whole
   // matrix fill about kSplitTargetGroups workgroups); the row's last part
