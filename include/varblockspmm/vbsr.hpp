@@ -8,7 +8,8 @@
 //    reads an invalid one out of bounds).
 //  - ScalarCsrPlan runs on rocSPARSE instead of cuSPARSE, and GroupedGemmPlan
 //    on rocBLAS (one batched GEMM per slot and block shape) instead of
-//    cuBLAS grouped GEMM.  The one-shot baseline helpers are not provided.
+//    cuBLAS grouped GEMM; the one-shot helpers keep the reference's names
+//    (cusparse_scalar_baseline runs the rocSPARSE plan).
 //  - Distribution gains Bimodal8or64 and Tied8to64; GeneratorOptions gains
 //    clamp_local_columns (clamped instead of cyclic local columns).
 //  - launch_row_owned takes the matrix's row schedule instead of the
@@ -294,6 +295,23 @@ inline bool split_row_advised(const Matrix& matrix, int rhs) {
 inline void launch_split_row(const Matrix& matrix, const float* B, float* C, int rhs, void* workspace,
                              int64_t workspace_bytes, hipStream_t stream) {
   detail::check(vbsr_launch_split_row(matrix.handle(), B, C, rhs, workspace, workspace_bytes, stream));
+}
+
+/** One-shot, synchronizing library baseline (reference vbsr.hpp:163-165):
+ * the rocSPARSE ScalarCsrPlan built, executed and released.  Prefer
+ * `ScalarCsrPlan` for repeated work. */
+inline void cusparse_scalar_baseline(const HostMatrix& matrix, const float* dB, float* dC, int rhs,
+                                     hipStream_t stream) {
+  const vbsr_host_view v = matrix.view();
+  detail::check(vbsr_scalar_csr_baseline(&v, dB, dC, rhs, stream));
+}
+
+/** One-shot, synchronizing grouped baseline (reference vbsr.hpp:166-168):
+ * the rocBLAS GroupedGemmPlan built, executed and released.  Prefer
+ * `GroupedGemmPlan` for reuse. */
+inline void slot_split_baseline(const HostMatrix& matrix, const float* dB, float* dC, int rhs, hipStream_t stream) {
+  const vbsr_host_view v = matrix.view();
+  detail::check(vbsr_slot_split_baseline(&v, dB, dC, rhs, stream));
 }
 
 /** The reference-order kernel (reference vbsr.hpp:161). */

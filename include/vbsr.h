@@ -298,6 +298,18 @@ int vbsr_gemm_plan_execute(vbsr_gemm_plan* plan, const float* B, float* C, hipSt
  * slots, i.e. the largest block-row degree (0 for a null plan). */
 int vbsr_gemm_plan_launch_count(const vbsr_gemm_plan* plan);
 
+/* cusparse_scalar_baseline (vbsr.hpp:163-165; cusparse_baseline.cu:183-188):
+ * one-shot and synchronising -- builds a ScalarCsrPlan for `host`, executes
+ * it on `stream`, waits for the stream and releases the plan.  Same checks
+ * and errors as vbsr_csr_plan_create / _execute.  Prefer the plan for
+ * repeated work. */
+int vbsr_scalar_csr_baseline(const vbsr_host_view* host, const float* B, float* C, int32_t rhs,
+                             hipStream_t stream);
+/* slot_split_baseline (vbsr.hpp:166-168; slot_split.cu:147-152): the same,
+ * one-shot and synchronising, with a GroupedGemmPlan. */
+int vbsr_slot_split_baseline(const vbsr_host_view* host, const float* B, float* C, int32_t rhs,
+                             hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

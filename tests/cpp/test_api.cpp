@@ -198,6 +198,13 @@ void run_case(vbsr::Distribution distribution, int degree, int rhs, bool local, 
   grouped.execute(b.ptr, c.ptr, stream);
   hip_ok(hipStreamSynchronize(stream), "sync");
   compare(c.read(), reference, bound, "grouped rocBLAS" + tag);
+  // The one-shot, synchronising forms (reference vbsr.hpp:163-168).
+  c.poison();
+  vbsr::cusparse_scalar_baseline(host, b.ptr, c.ptr, rhs, stream);
+  compare(c.read(), reference, bound, "one-shot rocSPARSE" + tag);
+  c.poison();
+  vbsr::slot_split_baseline(host, b.ptr, c.ptr, rhs, stream);
+  compare(c.read(), reference, bound, "one-shot grouped rocBLAS" + tag);
 
   hip_ok(hipStreamDestroy(stream), "hipStreamDestroy");
 }

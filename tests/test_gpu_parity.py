@@ -746,6 +746,27 @@ def test_grouped_gemm_plan_config3_and_empty_rows():
         c.close()
 
 
+@pytest.mark.parametrize("rhs", [8, 64])
+def test_one_shot_baselines(rhs):
+    """cusparse_scalar_baseline and slot_split_baseline (reference vbsr.hpp:163-168): one call builds the
+    plan, executes it, waits for the stream and releases it; the result equals the persistent plan's bit
+    for bit and is within tolerance of the oracle; an unsupported RHS is an invalid argument."""
+    note(f"one-shot baselines rhs={rhs}")
+    c = Case(vb.generate(40, 40, 4, "high", "random", 9), rhs, 9)
+    try:
+        for one_shot, plan_type in ((vb.cusparse_scalar_baseline, vb.ScalarCsrPlan),
+                                    (vb.slot_split_baseline, vb.GroupedGemmPlan)):
+            result = c.run(lambda: one_shot(c.host, c.b_dev, c.c_dev, rhs, c.stream))
+            c.check_tolerance(result, one_shot.__name__)
+            plan = plan_type(c.host, rhs)
+            assert run_csr(c, plan).tobytes() == result.tobytes()
+            plan.close()
+            with pytest.raises(ValueError):
+                one_shot(c.host, c.b_dev, c.c_dev[: c.host.scalar_rows * 12], 12, c.stream)
+    finally:
+        c.close()
+
+
 # ---- the largest B offsets ------------------------------------------------
 
 def largest_offset_case(scalar_cols, rhs):

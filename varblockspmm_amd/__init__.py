@@ -104,6 +104,8 @@ SIGNATURES = {
     "vbsr_gemm_plan_destroy": (None, [_P]),
     "vbsr_gemm_plan_execute": (ctypes.c_int, [_P, _P, _P, _P]),
     "vbsr_gemm_plan_launch_count": (ctypes.c_int, [_P]),
+    "vbsr_scalar_csr_baseline": (ctypes.c_int, [ctypes.POINTER(HostView), _P, _P, ctypes.c_int32, _P]),
+    "vbsr_slot_split_baseline": (ctypes.c_int, [ctypes.POINTER(HostView), _P, _P, ctypes.c_int32, _P]),
 }
 
 _lib = None
@@ -468,3 +470,23 @@ class GroupedGemmPlan:
 
     def workspace_bytes(self):
         return 0
+
+
+def cusparse_scalar_baseline(host, B, C, rhs, stream=None):
+    """One-shot, synchronising library baseline (reference cusparse_scalar_baseline, vbsr.hpp:163-165): the
+    rocSPARSE ScalarCsrPlan built, executed on `stream`, waited for and released."""
+    _check_panel(B, host.scalar_cols * int(rhs), "B")
+    _check_panel(C, host.scalar_rows * int(rhs), "C")
+    view = host._view()
+    _check(library().vbsr_scalar_csr_baseline(ctypes.byref(view), _address(B), _address(C), int(rhs),
+                                              _stream(stream)))
+
+
+def slot_split_baseline(host, B, C, rhs, stream=None):
+    """One-shot, synchronising grouped baseline (reference slot_split_baseline, vbsr.hpp:166-168): the rocBLAS
+    GroupedGemmPlan built, executed on `stream`, waited for and released."""
+    _check_panel(B, host.scalar_cols * int(rhs), "B")
+    _check_panel(C, host.scalar_rows * int(rhs), "C")
+    view = host._view()
+    _check(library().vbsr_slot_split_baseline(ctypes.byref(view), _address(B), _address(C), int(rhs),
+                                              _stream(stream)))

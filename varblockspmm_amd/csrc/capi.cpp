@@ -5,6 +5,8 @@
 #include <exception>
 #include <new>
 
+#include <hip/hip_runtime_api.h>
+
 #include "internal.hpp"
 
 struct vbsr_host_matrix {
@@ -276,5 +278,26 @@ int vbsr_gemm_plan_execute(vbsr_gemm_plan* plan, const float* B, float* C, hipSt
 }
 
 int vbsr_gemm_plan_launch_count(const vbsr_gemm_plan* plan) { return plan ? plan->plan.launch_count() : 0; }
+
+// The one-shot baselines build the plan, execute it and wait for the stream
+// before the plan (and its device copies) is released, as the reference's
+// do (cusparse_baseline.cu:183-188, slot_split.cu:147-152).
+int vbsr_scalar_csr_baseline(const vbsr_host_view* host, const float* B, float* C, int32_t rhs, hipStream_t stream) {
+  return guarded([&] {
+    require(host, "host");
+    vbsr_amd::CsrPlan plan(*host, rhs);
+    plan.execute(B, C, stream);
+    vbsr_amd::check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+  });
+}
+
+int vbsr_slot_split_baseline(const vbsr_host_view* host, const float* B, float* C, int32_t rhs, hipStream_t stream) {
+  return guarded([&] {
+    require(host, "host");
+    vbsr_amd::GemmPlan plan(*host, rhs);
+    plan.execute(B, C, stream);
+    vbsr_amd::check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+  });
+}
 
 }  // extern "C"
