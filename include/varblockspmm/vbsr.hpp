@@ -184,7 +184,7 @@ inline std::vector<float> cpu_reference(const HostMatrix& matrix, const std::vec
  * once), as in the reference.  SplitRow, reserved in the reference, is the
  * split-row path here: two launches and a plan-owned workspace, so one such
  * plan (or a copy of it, which shares the workspace) must not execute on two
- * streams at once. */
+ * streams at once, and must outlive any HIP graph captured from it. */
 enum class Kernel { Auto, RowOwned, SplitRow };
 
 /** Configuration for a reusable execution plan (reference vbsr.hpp:94-97). */

@@ -186,7 +186,9 @@ void vbsr_plan_destroy(vbsr_plan* plan);
  * `stream` (0 = null stream).  Allocates nothing.  A row-owned plan (AUTO,
  * ROW_OWNED) keeps no state, so its executes may run concurrently on any
  * streams.  A split-row plan's executes share its workspace: they must not
- * overlap in time (one stream, or events between streams). */
+ * overlap in time (one stream, or events between streams), and a HIP graph
+ * captured from one reads and writes that workspace, so the plan must
+ * outlive every replay of the graph. */
 int vbsr_plan_execute(const vbsr_plan* plan, const float* B, float* C, hipStream_t stream);
 /* Plan::launch_count (vbsr.hpp:112; plan.cpp:23-31): kernels enqueued by one
  * vbsr_plan_execute: 2 on the split-row path, else 1 (0 for a matrix
