@@ -1030,15 +1030,18 @@ def test_one_plan_on_two_streams_at_few_long_rows(kernel):
         matrix.close()
 
 
-@pytest.mark.parametrize("kernel", ["auto", "split_row"])
-def test_plan_execute_replays_from_a_hip_graph(kernel):
+@pytest.mark.parametrize("kernel,rhs,rows", [("auto", 32, 256), ("auto", 64, 2048), ("split_row", 32, 256)])
+def test_plan_execute_replays_from_a_hip_graph(kernel, rhs, rows):
     """execute enqueues its kernels (one, or two on the split-row path, which uses the plan's own
     workspace) and allocates nothing, so it can be captured into a HIP graph; every replay, with eager
-    work and synchronisations between replays, equals the eager result."""
-    host = vb.generate(256, 256, 8, "high", "random", 41)
-    c = Case(host, 32, 41)
+    work and synchronisations between replays, equals the eager result.  At RHS 64 and 2048 rows the
+    plan runs the tile-split kernel."""
+    host = vb.generate(rows, rows, 8, "high", "random", 41)
+    c = Case(host, rhs, 41)
     try:
-        plan = vb.Plan(c.matrix, 32, kernel)
+        if rhs == 64:
+            assert c.matrix.row_schedule().rhs64_tiles == 1
+        plan = vb.Plan(c.matrix, rhs, kernel)
         assert plan.launch_count() == (2 if kernel == "split_row" else 1)
         eager = c.run_plan(plan)
         c.check_tolerance(eager, "eager")
