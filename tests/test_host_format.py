@@ -189,6 +189,27 @@ def test_launchers_reject_null_and_overlapping_panels_before_touching_the_gpu():
                 launch(b, cc)
 
 
+def test_launchers_reject_a_schedule_without_its_launch_order_before_touching_the_gpu():
+    """A schedule is the matrix's own (vbsr_matrix_row_schedule), whose every launch order holds at
+    least one workgroup when the matrix has block rows.  A zeroed struct, or one whose RHS 64 choice
+    (rhs64_tiles) names an order it does not hold, is refused on the host instead of launching
+    nothing or reading through a null pointer.  Addresses here are never dereferenced."""
+    view = vb.DeviceView()
+    view.block_rows, view.scalar_rows, view.scalar_cols = 4, 96, 80
+    b, c = 0x7f0000000000, 0x7f0000100000
+    for rhs in (8, 16, 32, 64):
+        with pytest.raises(ValueError, match="launch order"):
+            vb.launch_row_owned(view, vb.RowSchedule(), b, c, rhs)
+    fake = 0x7f0000200000
+    for rows_tile, groups_tile in ((None, 0), (fake, 0), (None, 8)):
+        s = vb.RowSchedule()
+        s.steps = s.rows = s.rows_wide = s.rows_rhs64 = fake
+        s.groups = s.groups_rhs64 = 8
+        s.rows_tile, s.groups_tile, s.rhs64_tiles = rows_tile, groups_tile, 1
+        with pytest.raises(ValueError, match="launch order"):
+            vb.launch_row_owned(view, s, b, c, 64)
+
+
 def test_launchers_check_torch_panels_before_touching_the_gpu():
     """The Python launchers check what the C ABI cannot see: a torch panel must be a contiguous
     float32 device tensor of exactly scalar_cols * rhs (B) or scalar_rows * rhs (C) floats."""

@@ -791,13 +791,18 @@ void launch_row_owned_math(const vbsr_device_view& a, const vbsr_row_schedule& s
   int64_t groups = s.groups;
   const bool tiles = !kValu && rhs == 64 && s.rhs64_tiles != 0;
   if (tiles) {
-    if (s.rows_tile == nullptr && s.groups_tile > 0) throw std::invalid_argument("schedule without a tile order");
     rows = s.rows_tile;
     groups = s.groups_tile;
   } else if (rhs == 64 && s.rows_rhs64 != nullptr) {
     rows = s.rows_rhs64;
     groups = s.groups_rhs64;
   }
+  // A matrix with block rows has at least one workgroup in every order (empty
+  // rows included), so a schedule whose chosen order is missing or empty
+  // belongs to no matrix with rows: refuse it rather than launch nothing or
+  // read through a null pointer.
+  if (a.block_rows > 0 && (rows == nullptr || groups <= 0 || s.steps == nullptr))
+    throw std::invalid_argument("schedule has no launch order for this matrix (take it from vbsr_matrix_row_schedule)");
   const Launch L{a, static_cast<const StepRec*>(s.steps), static_cast<const WaveItem*>(rows), s.step_limit, b, c,
                  a.scalar_rows};
   // At RHS 64 the schedule says which kernel runs: the split-k kernel or
