@@ -800,11 +800,12 @@ def check_against_oracle(host, b, rhs, result, name):
     assert normwise <= NORMWISE_TOL and rel_l2 <= REL_L2_TOL and elementwise <= ELEMENTWISE_TOL, name
 
 
-@pytest.mark.parametrize("scalar_cols,rhs", [(71_582_784, 16), (153_391_680, 8)])
+@pytest.mark.parametrize("scalar_cols,rhs", [(71_582_784, 16), (153_391_680, 8), (71_582_784, 64)])
 def test_largest_b_offsets_take_the_mfma_kernel(scalar_cols, rhs):
     """The largest K (in whole 64-wide block columns) the MFMA kernel takes: its 32-bit B offsets
     within a 16-column tile reach (min(rhs, 16) - 1) * K * 4 + 64 bytes, 64 bytes or more below
-    the out-of-range offset 0xfffffff0."""
+    the out-of-range offset 0xfffffff0.  At RHS 64 both the split-k kernel and the tile split
+    (forced through the schedule's rhs64_tiles) read every 16-column tile at those offsets."""
     note(f"largest offsets: K={scalar_cols} rhs={rhs} (B {scalar_cols * rhs * 4 / 2**30:.1f} GiB)")
     host, b = largest_offset_case(scalar_cols, rhs)
     matrix = vb.Matrix(host)
@@ -817,6 +818,16 @@ def test_largest_b_offsets_take_the_mfma_kernel(scalar_cols, rhs):
             vb.launch_row_owned(matrix.device_view(), matrix.row_schedule(), b_dev, c_dev, rhs, stream)
         stream.synchronize()
         check_against_oracle(host, b, rhs, c_dev.cpu().numpy(), "launch_row_owned")
+        if rhs == 64:
+            for tiles in (0, 1):
+                schedule = matrix.row_schedule()
+                schedule.rhs64_tiles = tiles
+                c_dev.fill_(float("nan"))
+                torch.cuda.synchronize()
+                with torch.cuda.stream(stream):
+                    vb.launch_row_owned(matrix.device_view(), schedule, b_dev, c_dev, rhs, stream)
+                stream.synchronize()
+                check_against_oracle(host, b, rhs, c_dev.cpu().numpy(), f"launch_row_owned, rhs64_tiles={tiles}")
         c_dev.fill_(float("nan"))
         torch.cuda.synchronize()
         plan = vb.Plan(matrix, rhs)
@@ -830,13 +841,14 @@ def test_largest_b_offsets_take_the_mfma_kernel(scalar_cols, rhs):
         matrix.close()
 
 
-@pytest.mark.parametrize("scalar_cols,rhs", [(71_582_848, 16), (153_391_744, 8)])
+@pytest.mark.parametrize("scalar_cols,rhs", [(71_582_848, 16), (153_391_744, 8), (71_582_848, 64)])
 def test_k_past_the_offset_limit_stays_on_the_mfma_kernel(scalar_cols, rhs):
     """One block column past the largest K the 32-bit B offsets reach: launch_row_owned and the plan
     address B with 64-bit lane pointers instead, match the oracle, agree bit for bit with
     launch_row_owned_wide_b and with each other, and repeat bit for bit; the split-row path (same
     kernel, over row parts) matches the oracle too; the VALU variant, which keeps the offset bound,
-    refuses the matrix."""
+    refuses the matrix.  At RHS 64 the same holds for the split-k kernel and the tile split, each
+    forced through the schedule's rhs64_tiles."""
     note(f"past the offset limit: K={scalar_cols} rhs={rhs} (B {scalar_cols * rhs * 4 / 2**30:.1f} GiB)")
     host, b = largest_offset_case(scalar_cols, rhs)
     matrix = vb.Matrix(host)
@@ -865,6 +877,14 @@ def test_k_past_the_offset_limit_stays_on_the_mfma_kernel(scalar_cols, rhs):
         assert planned.tobytes() == first.tobytes(), "plan differs from launch_row_owned"
         split = run(lambda: vb.launch_split_row_static(matrix, b_dev, c_dev, rhs, stream))
         check_against_oracle(host, b, rhs, split, "split-row path past the limit")
+        if rhs == 64:
+            for tiles in (0, 1):
+                forced = matrix.row_schedule()
+                forced.rhs64_tiles = tiles
+                got = run(lambda: vb.launch_row_owned(view, forced, b_dev, c_dev, rhs, stream))
+                check_against_oracle(host, b, rhs, got, f"rhs64_tiles={tiles} past the limit")
+                wide_forced = run(lambda: vb.launch_row_owned_wide_b(view, forced, b_dev, c_dev, rhs, stream))
+                assert wide_forced.tobytes() == got.tobytes(), f"rhs64_tiles={tiles}: wide form differs"
         with pytest.raises(ValueError):
             vb.launch_row_owned_valu(view, schedule, b_dev, c_dev, rhs, stream)
         plan.close()
