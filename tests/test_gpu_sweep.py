@@ -1,7 +1,8 @@
 """GPU parity over the whole regime sweep, at its full size and at a reduced
 size, plus the benchmark executable and the sweep runner end to end.
 
-Configuration 5's 128 cases run at their own size (4096 block rows) against
+Configuration 5's 128 cases, and the 128 instances of the reference's
+publication grid at seed 1, run at their own size (4096 block rows) against
 the threaded oracle.
 
 Every case of both grids (the 128-case config-5 sweep, with seed = case
@@ -66,16 +67,12 @@ THREADS = max(1, min(16, int(os.environ.get("OMP_NUM_THREADS", "8"))))
 CONFIG5 = list(enumerate(run_grid.cases("config5")))
 
 
-@pytest.mark.parametrize("index,case", CONFIG5,
-                         ids=[f"{i}-{c['distribution']}-{c['locality']}-d{c['degree']}-n{c['rhs']}" for i, c in CONFIG5])
-def test_config5_full_size_parity(index, case):
-    """BASELINE configuration 5 at its own size: each of the 128 cases at 4096 block rows (the generator
-    makes a different matrix at another row count, not a smaller copy), Plan::execute checked against the
-    oracle's cpu_reference (rows over OpenMP threads, bit-identical to the serial one) with the bars of
+def check_full_size(case):
+    """Plan::execute on the case's matrix at FULL_ROWS block rows, checked against the oracle's
+    cpu_reference (rows over OpenMP threads, bit-identical to the serial one) with the bars of
     test_gpu_parity.py, and bit-stable across two runs.  B is the reference test's generator with the
     case's seed."""
     rhs, seed = case["rhs"], case["seed"]
-    note(f"config5 full size case {index}: {case}")
     host = vb.generate(FULL_ROWS, FULL_ROWS, case["degree"], case["distribution"], case["locality"], seed)
     oracle = o.HostMatrix(host.block_rows, host.block_cols, **host.arrays())
     b = o.make_random_input(host.scalar_cols * rhs, seed)
@@ -105,6 +102,30 @@ def test_config5_full_size_parity(index, case):
         assert normwise <= NORMWISE_TOL and rel_l2 <= REL_L2_TOL and elementwise <= ELEMENTWISE_TOL
     finally:
         matrix.close()
+
+
+@pytest.mark.parametrize("index,case", CONFIG5,
+                         ids=[f"{i}-{c['distribution']}-{c['locality']}-d{c['degree']}-n{c['rhs']}" for i, c in CONFIG5])
+def test_config5_full_size_parity(index, case):
+    """BASELINE configuration 5 at its own size: each of the 128 cases at 4096 block rows (the generator
+    makes a different matrix at another row count, not a smaller copy)."""
+    note(f"config5 full size case {index}: {case}")
+    check_full_size(case)
+
+
+REFERENCE_GRID = list(enumerate(run_grid.cases("reference", seed=1)))
+
+
+@pytest.mark.parametrize("index,case", REFERENCE_GRID,
+                         ids=[f"{i}-{c['distribution']}-{c['locality']}-d{c['degree']}-n{c['rhs']}"
+                              for i, c in REFERENCE_GRID])
+def test_reference_grid_full_size_parity(index, case):
+    """The reference's publication grid (scripts/run_grid.sh:11-14) at seed 1: the 128 instances of
+    data/publication/regime_map_seed1.csv (the same matrices: tests/test_oracle.py checks their
+    Sigma h*w against that file), each at 4096 block rows, with the reference generator's own
+    distributions and cyclic local columns."""
+    note(f"reference grid full size case {index}: {case}")
+    check_full_size(case)
 
 
 def test_benchmark_executable_end_to_end():
