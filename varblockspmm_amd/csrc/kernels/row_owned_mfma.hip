@@ -32,8 +32,9 @@
 // step's k range of each B column.  Lanes that must contribute nothing get
 // zeros from the hardware range check instead of from extra instructions:
 // in a half step A columns 8-15 lie past the 8-column resource and the B
-// lanes holding k0 + 8 .. k0 + 15 use an offset past every resource; a step
-// beyond a wave's last one gets zero-byte resources.  Those lanes therefore
+// lanes holding k0 + 8 .. k0 + 15 use an offset past every resource (so do
+// the B lanes of columns 8-15 at RHS 8); a step beyond a wave's last one gets
+// zero-byte resources.  Those lanes therefore
 // feed 0 * 0, so each k enters once and non-finite inputs reach C exactly as
 // in the reference.  B's offsets within a 16-column tile are 32-bit; past
 // that bound on K (narrow_b_offsets) the kWideB instantiation reads B at the
@@ -349,12 +350,14 @@ __device__ __forceinline__ void row_body(const Launch& L, const WaveItem& item, 
   const uint32_t a_full_bytes = uint32_t(16 * h) * 4u;
   const uint32_t a_half_bytes = uint32_t(8 * h) * 4u;
 
-  // B load layout: lane 4n + q reads B[k0 + 4q .. k0 + 4q + 3, n0 + n] (rhs
-  // columns past RHS read a duplicate column; in a half step q = 2, 3 read
-  // nothing).
+  // B load layout: lane 4n + q reads B[k0 + 4q .. k0 + 4q + 3, n0 + n] (at
+  // RHS 8 the lanes of columns 8-15 read nothing, and in a half step q = 2, 3
+  // read nothing: those lanes hold zeros, and the outputs they feed are never
+  // stored).
   const int b_n = lane >> 2;
   const int b_q = lane & 3;
-  const uint32_t b_full = uint32_t(b_n & (kRhsLanes - 1)) * ldb * 4u + uint32_t(16 * b_q);
+  const bool b_column = b_n < kRhsLanes;
+  const uint32_t b_full = b_column ? uint32_t(b_n) * ldb * 4u + uint32_t(16 * b_q) : kOutOfRange;
   const uint32_t b_half = b_q < 2 ? b_full : kOutOfRange;
   const uint32_t b_span = uint32_t(kRhsLanes - 1) * ldb * 4u;  // a B tile's bytes before its last column
   const int64_t ldb_wide = L.a.scalar_cols;
@@ -395,8 +398,9 @@ __device__ __forceinline__ void row_body(const Launch& L, const WaveItem& item, 
       const float* b_base = L.b + (b_word & kOffsetMask);
       if constexpr (kWideB) {
         // The same addresses as the buffer loads below; the lanes those give
-        // zeros (a dead step, the upper half of a half step) load nothing.
-        const bool take = live && (!half || b_q < 2);
+        // zeros (a dead step, the upper half of a half step, columns past
+        // RHS 8) load nothing.
+        const bool take = live && (!half || b_q < 2) && b_column;
 #pragma unroll
         for (int nt = 0; nt < kRhsTiles; ++nt) {
           st.b[nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
